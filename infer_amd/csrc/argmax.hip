@@ -1,0 +1,287 @@
+// argmax.hip -- decode LM-head GEMV with fused greedy selection (QwenGemmArgmax) on gfx950.
+//
+// Semantics (src/kernel/common/qwen_gemm_argmax.cc:28-49, x86/linear.cc:603-648): per vocabulary row
+// v, s_v = fp32 dot(a, w_v); the value compared is BF16(s_v) (RNE, NaN quieted); NaN values are
+// skipped; the first strict maximum wins, so equal values -- including +0 and -0 -- keep the lowest
+// index; when every value is NaN the token is 0.
+// FP8 head (x86/linear_fp8.cc:757-788; the exported Gemm -> Cast(bf16) pair): the value compared is
+// BF16(Dec(Enc(s_v / out_scale)) * out_scale).
+//
+// Selection is a max over 64-bit keys  (order(bf16) << 32) | (0xffffffff - v):  `order` maps BF16
+// bits to an unsigned key monotone in the value with +0/-0 merged, NaN never enters, and a larger
+// low word means a lower index.  Key 0 means "no candidate".
+//
+// Layout of the work: the weight [V][K] streams once from HBM with 16-byte loads; each wave owns a
+// strip of rows and keeps R rows in flight; the activation rows (m <= 16) stay in registers as raw
+// BF16/FP8 bits.  Each block publishes one key per activation row to a partials array, and the
+// last block to finish (atomic ticket) reduces the partials, writes the int64 tokens and re-arms
+// the ticket, so the kernel is replay-safe with no memset.
+#include "fhip_internal.h"
+#include "codec.h"
+
+namespace {
+
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kRows = 4;  // weight rows per wave iteration
+
+__device__ __forceinline__ unsigned long long make_key(uint16_t bf, int64_t idx) {
+    if ((bf & 0x7f80u) == 0x7f80u && (bf & 0x7fu) != 0u) return 0ull;  // NaN: never selected
+    uint32_t u = bf;
+    if ((u & 0x7fffu) == 0u) u = 0u;                                    // -0 == +0
+    const uint32_t order = (u & 0x8000u) ? (~u & 0xffffu) : (u | 0x8000u);
+    return ((unsigned long long)order << 32) | (unsigned long long)(0xffffffffu - (uint32_t)idx);
+}
+
+__device__ __forceinline__ int64_t key_index(unsigned long long key) {
+    return key == 0ull ? 0 : (int64_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
+}
+
+__device__ __forceinline__ unsigned long long wave_max(unsigned long long v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long o = __shfl_xor(v, off, 64);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// Element type of the head: BF16 (2 B) or FP8 (1 B).  One 16-byte load = 8 BF16 or 16 FP8 values.
+template <int KIND>  // 0 = BF16, 1 = FP8 e4m3, 2 = FP8 e5m2
+struct Head {
+    static constexpr int kPer16 = KIND == 0 ? 8 : 16;
+    __device__ static __forceinline__ void decode(const uint4& v, float* f) {
+        if constexpr (KIND == 0) {
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                f[2 * i] = __uint_as_float(w[i] << 16);
+                f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+            }
+        } else {
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v2f lo, hi;
+                if constexpr (KIND == 2) {
+                    lo = __builtin_amdgcn_cvt_pk_f32_bf8((int)w[i], false);
+                    hi = __builtin_amdgcn_cvt_pk_f32_bf8((int)w[i], true);
+                } else {
+                    lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], false);
+                    hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], true);
+                }
+                f[4 * i] = lo.x;
+                f[4 * i + 1] = lo.y;
+                f[4 * i + 2] = hi.x;
+                f[4 * i + 3] = hi.y;
+            }
+        }
+    }
+};
+
+struct HeadParams {
+    float ab_scale;   // FP8: a_scale * w_scale
+    float out_scale;  // FP8: output scale
+    float* logits;    // optional [m][v]
+};
+
+template <int KIND, int MT, int kMaxT>
+__global__ __launch_bounds__(kThreads) void gemv_argmax_kernel(const uint8_t* __restrict__ a, int64_t m, int64_t k,
+                                                               const uint8_t* __restrict__ w, int64_t v,
+                                                               HeadParams hp, unsigned long long* __restrict__ partials,
+                                                               ArgmaxScratch* __restrict__ scratch,
+                                                               int64_t* __restrict__ tokens) {
+    using H = Head<KIND>;
+    constexpr int esize = KIND == 0 ? 2 : 1;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t row_bytes = k * esize;
+    const int64_t chunks = row_bytes / 16;  // host guarantees k * esize % 16 == 0
+    // Activation chunks this lane covers: c = lane + 64*t, t < kMaxT (k * esize <= kMaxT KiB).
+    uint4 xa[MT][kMaxT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j)
+#pragma unroll
+        for (int t = 0; t < kMaxT; ++t) {
+            const int64_t c = lane + 64 * t;
+            xa[j][t] = (j < m && c < chunks) ? *reinterpret_cast<const uint4*>(a + j * row_bytes + c * 16)
+                                             : make_uint4(0, 0, 0, 0);
+        }
+
+    unsigned long long best[MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) best[j] = 0ull;
+
+    const int64_t total_waves = (int64_t)gridDim.x * kWaves;
+    for (int64_t r0 = ((int64_t)blockIdx.x * kWaves + wave) * kRows; r0 < v; r0 += total_waves * kRows) {
+        float acc[kRows][MT];
+#pragma unroll
+        for (int r = 0; r < kRows; ++r)
+#pragma unroll
+            for (int j = 0; j < MT; ++j) acc[r][j] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < kMaxT; ++t) {
+            const int64_t c = lane + 64 * t;
+            if (c < chunks) {
+                uint4 wv[kRows];
+#pragma unroll
+                for (int r = 0; r < kRows; ++r) {
+                    const int64_t row = r0 + r < v ? r0 + r : v - 1;
+                    wv[r] = *reinterpret_cast<const uint4*>(w + row * row_bytes + c * 16);
+                }
+#pragma unroll
+                for (int j = 0; j < MT; ++j) {
+                    float xf[H::kPer16];
+                    H::decode(xa[j][t], xf);
+#pragma unroll
+                    for (int r = 0; r < kRows; ++r) {
+                        float wf[H::kPer16];
+                        H::decode(wv[r], wf);
+                        float s = acc[r][j];
+#pragma unroll
+                        for (int i = 0; i < H::kPer16; ++i) s += xf[i] * wf[i];
+                        acc[r][j] = s;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+#pragma unroll
+            for (int j = 0; j < MT; ++j) {
+                float s = acc[r][j];
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+                const int64_t row = r0 + r;
+                if (row < v && j < m) {
+                    uint16_t bf;
+                    if constexpr (KIND == 0) {
+                        bf = fhip::bf16_encode(s);
+                    } else {
+                        const uint8_t code = fhip::fp8_encode(s * hp.ab_scale / hp.out_scale, KIND == 2);
+                        s = fhip::fp8_decode(code, KIND == 2) * hp.out_scale;
+                        bf = fhip::bf16_encode(s);
+                    }
+                    const unsigned long long key = make_key(bf, row);
+                    best[j] = key > best[j] ? key : best[j];
+                    if (hp.logits != nullptr && lane == 0) hp.logits[j * v + row] = s;
+                }
+            }
+        }
+    }
+
+    // Block reduction -> partials[block][j]
+    __shared__ unsigned long long red[kWaves][MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) {
+        const unsigned long long b = wave_max(best[j]);
+        if (lane == 0) red[wave][j] = b;
+    }
+    __syncthreads();
+    __shared__ bool last;
+    if (threadIdx.x == 0) {
+        for (int j = 0; j < MT; ++j) {
+            unsigned long long b = red[0][j];
+            for (int q = 1; q < kWaves; ++q) b = red[q][j] > b ? red[q][j] : b;
+            partials[(int64_t)blockIdx.x * MT + j] = b;
+        }
+        __threadfence();
+        const unsigned int ticket = atomicAdd(&scratch->done, 1u);
+        last = ticket == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    // Last block: reduce the partials of every block.
+    for (int j = 0; j < MT; ++j) {
+        unsigned long long b = 0ull;
+        for (int64_t q = threadIdx.x; q < gridDim.x; q += kThreads) {
+            const unsigned long long p = __hip_atomic_load(&partials[q * MT + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            b = p > b ? p : b;
+        }
+        b = wave_max(b);
+        if (lane == 0) red[wave][j] = b;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int j = 0; j < MT && j < m; ++j) {
+            unsigned long long b = red[0][j];
+            for (int q = 1; q < kWaves; ++q) b = red[q][j] > b ? red[q][j] : b;
+            tokens[j] = key_index(b);
+        }
+        scratch->done = 0u;  // re-arm for the next call / graph replay
+    }
+}
+
+template <int KIND>
+int launch(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k, const uint8_t* w, int64_t v, HeadParams hp,
+           int64_t* tokens, const char* name) {
+    int dev_cus = 256;
+    (void)hipDeviceGetAttribute(&dev_cus, hipDeviceAttributeMultiprocessorCount, ctx->device);
+    const int64_t rows_per_block = (int64_t)kWaves * kRows;
+    int64_t grid = (v + rows_per_block - 1) / rows_per_block;
+    const int64_t cap = (int64_t)dev_cus * 8;  // persistent-ish: a few blocks per CU, grid-stride
+    if (grid > cap) grid = cap;
+    void* ws = nullptr;
+    int rc = fhip::acquire_workspace(ctx, (size_t)grid * 16 * sizeof(unsigned long long), &ws);
+    if (rc != FHIP_OK) return rc;
+    auto* partials = static_cast<unsigned long long*>(ws);
+    const int64_t bytes = k * (KIND == 0 ? 2 : 1);
+    const int t = bytes <= 1024 ? 1 : (bytes <= 2048 ? 2 : 4);
+#define FHIP_ARGMAX_CASE(MT, T)                                                                                   \
+    if (m <= MT && t == T) {                                                                                      \
+        gemv_argmax_kernel<KIND, MT, T><<<(unsigned)grid, kThreads, 0, ctx->stream>>>(a, m, k, w, v, hp, partials, \
+                                                                                      ctx->scratch, tokens);     \
+        ctx->last_backend = name;                                                                                 \
+        FHIP_CHECK_LAUNCH(ctx, "gemv_argmax_kernel");                                                             \
+        return FHIP_OK;                                                                                           \
+    }
+    FHIP_ARGMAX_CASE(1, 1)
+    FHIP_ARGMAX_CASE(1, 2)
+    FHIP_ARGMAX_CASE(1, 4)
+    FHIP_ARGMAX_CASE(8, 1)
+    FHIP_ARGMAX_CASE(8, 2)
+    FHIP_ARGMAX_CASE(8, 4)
+    FHIP_ARGMAX_CASE(16, 1)
+    FHIP_ARGMAX_CASE(16, 2)
+    FHIP_ARGMAX_CASE(16, 4)
+#undef FHIP_ARGMAX_CASE
+    return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "gemv_argmax: m > 16");
+}
+
+}  // namespace
+
+extern "C" {
+
+int fhip_bf16_gemv_argmax(fhip_context ctx, const uint16_t* a, int64_t m, int64_t k, const uint16_t* w, int64_t v,
+                          int64_t* tokens, float* logits) {
+    if (!ctx) return FHIP_ERR_INVALID;
+    if (!a || !w || !tokens || m <= 0 || k <= 0 || v <= 0) return fhip::set_error(ctx, FHIP_ERR_INVALID, "bf16_gemv_argmax: bad arguments");
+    if (m > kArgmaxMaxRows || (k * 2) % 16 != 0 || k * 2 > 4096 || v >= (int64_t(1) << 32))
+        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "bf16_gemv_argmax: needs m <= 16, k % 8 == 0, k <= 2048");
+    if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(w)) & 15)
+        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "bf16_gemv_argmax: pointers must be 16-byte aligned");
+    HeadParams hp{1.0f, 1.0f, logits};
+    return launch<0>(ctx, reinterpret_cast<const uint8_t*>(a), m, k, reinterpret_cast<const uint8_t*>(w), v, hp, tokens,
+                     "bf16_gemv_argmax");
+}
+
+int fhip_fp8_gemv_argmax(fhip_context ctx, int dtype, const uint8_t* a, float a_scale, int64_t m, int64_t k,
+                         const uint8_t* w, float w_scale, int64_t v, float out_scale, int64_t* tokens) {
+    if (!ctx) return FHIP_ERR_INVALID;
+    if (!a || !w || !tokens || m <= 0 || k <= 0 || v <= 0 || (dtype != FHIP_FP8E4M3 && dtype != FHIP_FP8E5M2))
+        return fhip::set_error(ctx, FHIP_ERR_INVALID, "fp8_gemv_argmax: bad arguments");
+    if (!fhip::valid_scale(a_scale) || !fhip::valid_scale(w_scale) || !fhip::valid_scale(out_scale))
+        return fhip::set_error(ctx, FHIP_ERR_INVALID, "fp8_gemv_argmax: scales must be finite and positive");
+    if (m > kArgmaxMaxRows || k % 16 != 0 || k > 4096 || v >= (int64_t(1) << 32))
+        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "fp8_gemv_argmax: needs m <= 16, k % 16 == 0, k <= 4096");
+    if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(w)) & 15)
+        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "fp8_gemv_argmax: pointers must be 16-byte aligned");
+    HeadParams hp{a_scale * w_scale, out_scale, nullptr};
+    if (dtype == FHIP_FP8E5M2) return launch<2>(ctx, a, m, k, w, v, hp, tokens, "fp8e5m2_gemv_argmax");
+    return launch<1>(ctx, a, m, k, w, v, hp, tokens, "fp8e4m3_gemv_argmax");
+}
+
+}  // extern "C"

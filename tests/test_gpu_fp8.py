@@ -1,0 +1,163 @@
+"""GPU parity of the FP8 path (Cast, decode GEMV, prefill MFMA GEMM) against the oracle.
+
+Oracle: oracle/feather_oracle.c (Common semantics, src/kernel/common/matmul.cc:56-130, gemm.cc:62-100,
+cast.cc:62-165).  Tolerance (FP8 outputs): every element within 1 FP8 code of the oracle (the fp32
+accumulation order differs) or, for sums near zero, within the fp32 summation-order bound (see
+tests/common.py fp8_linear_check); the exact-match rate is printed.  Cast is bit-exact.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import pyoracle as po
+from tests.common import SEEDS, fp8_code_distance, fp8_linear_check, fp8_tensor, rng, same_float_bits
+
+pytestmark = pytest.mark.gpu
+
+FP8 = [po.FP8E4M3, po.FP8E5M2]
+
+
+def dev(a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a).cuda()
+
+
+def host(t, dtype=None):
+    a = t.cpu().numpy()
+    if dtype is not None:
+        a = a.view(dtype)
+    return a
+
+
+@pytest.mark.parametrize("dtype", FP8)
+def test_cast_fp8_decode_all_codes(ctx, dtype):
+    codes = np.arange(256, dtype=np.uint8)
+    out = torch.empty(256, dtype=torch.float32, device="cuda")
+    ctx.cast(dev(codes), dtype, 0.5, out, po.FP32, 1.0)
+    ref = po.cast_from_fp8(dtype, codes, 0.5, po.FP32)
+    got = host(out)
+    bad = [(hex(c), float(got[c]), float(ref[c])) for c in range(256) if not same_float_bits(got[c:c + 1], ref[c:c + 1])]
+    assert not bad, bad[:16]
+    out16 = torch.empty(256, dtype=torch.int16, device="cuda")
+    ctx.cast(dev(codes), dtype, 0.25, out16, po.BF16, 1.0)
+    assert np.array_equal(host(out16, np.uint16), po.cast_from_fp8(dtype, codes, 0.25, po.BF16))
+
+
+@pytest.mark.parametrize("dtype", FP8)
+def test_cast_encode_float_patterns(ctx, dtype):
+    # every sign/exponent with the top 12 mantissa bits swept and boundary low bits, plus specials
+    hi = np.arange(1 << 21, dtype=np.uint32) << 11
+    lows = np.array([0, 1, 0x3FF, 0x400, 0x401, 0x7FF], dtype=np.uint32)
+    bits = (hi[:, None] | lows[None, :]).reshape(-1)
+    x = bits.view(np.float32)
+    for scale in (1.0, 0.0078125, 3.0):
+        out = torch.empty(x.size, dtype=torch.uint8, device="cuda")
+        ctx.cast(dev(x), po.FP32, 1.0, out, dtype, scale)
+        ref = po.cast_to_fp8(po.FP32, x, dtype, scale)
+        bad = np.nonzero(host(out) != ref)[0]
+        assert bad.size == 0, f"scale {scale}: {bad.size} mismatches, first bits {bits[bad[:4]]}"
+
+
+def _linear_case(seed, dtype, m, k, n, layout):
+    r = rng(seed)
+    x = r.standard_normal((m, k)).astype(np.float32)
+    w = (r.standard_normal((n, k)) * 0.02).astype(np.float32)
+    a_codes, sa = fp8_tensor(x, dtype)
+    w_codes, sw = fp8_tensor(w, dtype)  # [N,K]
+    sums = po.fp8_sums(dtype, a_codes, sa, w_codes, sw, True)
+    from tests.common import fp8_pow2_scale
+    s_out = fp8_pow2_scale(float(np.max(np.abs(sums))), dtype)
+    w_src = w_codes if layout == 1 else np.ascontiguousarray(w_codes.T)
+    return a_codes, sa, w_codes, w_src, sw, s_out
+
+
+@pytest.mark.parametrize("dtype", FP8)
+@pytest.mark.parametrize("m", [1, 3, 4, 16])
+@pytest.mark.parametrize("layout", [0, 1])
+def test_fp8_gemv_matches_oracle(ctx, dtype, m, layout):
+    k, n = 1024, 3584
+    a, sa, w_nk, w_src, sw, s_out = _linear_case(SEEDS[2] + m, dtype, m, k, n, layout)
+    wt = ctx.prepare_weight(dev(w_src), dtype, k, n, layout, version=1)
+    out = torch.empty((m, n), dtype=torch.uint8, device="cuda")
+    ctx.fp8_linear(dev(a), dtype, sa, m, wt, sw, out, dtype, s_out)
+    assert ctx.last_backend().startswith("fp8_gemv")
+    ref = po.fp8_gemm(dtype, a, sa, w_nk, sw, True, s_out)
+    fp8_linear_check(dtype, host(out), ref, a, sa, w_nk, sw, s_out, f"gemv m={m}")
+    wt.release()
+
+
+@pytest.mark.parametrize("dtype", FP8)
+def test_fp8_gemv_fused_bf16_io(ctx, dtype):
+    """bf16 activations -> Cast(fp8) -> MatMul -> Cast(bf16), fused: equals the three-node chain."""
+    m, k, n = 4, 1024, 3584
+    r = rng(SEEDS[2])
+    x = r.standard_normal((m, k)).astype(np.float32)
+    xb = po.bf16_encode(x)
+    w = (r.standard_normal((k, n)) * 0.02).astype(np.float32)
+    w_codes, sw = fp8_tensor(w, dtype)  # [K,N] MatMul layout
+    from tests.common import fp8_pow2_scale
+    s_in = fp8_pow2_scale(float(np.max(np.abs(po.bf16_decode(xb)))), dtype)
+    a_codes = po.cast_to_fp8(po.BF16, xb, dtype, s_in)
+    s_out = fp8_pow2_scale(float(np.max(np.abs(po.fp8_sums(dtype, a_codes, s_in, w_codes, sw, False)))), dtype)
+    wt = ctx.prepare_weight(dev(w_codes), dtype, k, n, 0, version=2)
+    out = torch.empty((m, n), dtype=torch.int16, device="cuda")
+    ctx.fp8_linear(dev(xb), po.BF16, s_in, m, wt, sw, out, po.BF16, s_out)
+    ref_codes = po.fp8_matmul(dtype, a_codes, s_in, w_codes, sw, s_out)
+    ref = po.cast_from_fp8(dtype, ref_codes, s_out, po.BF16)
+    got = host(out, np.uint16)
+    got_codes = po.cast_to_fp8(po.BF16, got, dtype, s_out)  # bf16 of an fp8 value re-encodes exactly
+    assert np.array_equal(po.cast_from_fp8(dtype, got_codes, s_out, po.BF16), got)
+    fp8_linear_check(dtype, got_codes, ref_codes, a_codes, s_in, np.ascontiguousarray(w_codes.T), sw, s_out,
+                     "fused bf16")
+    assert np.mean(got == ref) > 0.97
+    wt.release()
+
+
+@pytest.mark.parametrize("dtype", FP8)
+@pytest.mark.parametrize("shape", [(256, 1024, 512), (100, 384, 200), (4096, 1024, 3584)])
+def test_fp8_mfma_gemm_matches_oracle(ctx, dtype, shape):
+    m, k, n = shape
+    a, sa, w_nk, w_src, sw, s_out = _linear_case(SEEDS[3] + m, dtype, m, k, n, 1)
+    if m * n > 1 << 21:
+        # full-size case: check a seeded subset of rows against the oracle
+        rows = np.sort(rng(7).choice(m, 96, replace=False))
+    else:
+        rows = np.arange(m)
+    wt = ctx.prepare_weight(dev(w_src), dtype, k, n, 1, version=3)
+    out = torch.empty((m, n), dtype=torch.uint8, device="cuda")
+    ctx.fp8_linear(dev(a), dtype, sa, m, wt, sw, out, dtype, s_out)
+    assert ctx.last_backend().startswith("fp8_mfma_gemm")
+    ref = po.fp8_gemm(dtype, a[rows], sa, w_nk, sw, True, s_out)
+    fp8_linear_check(dtype, host(out)[rows], ref, a[rows], sa, w_nk, sw, s_out, f"gemm {shape}")
+    wt.release()
+
+
+def test_fp8_gemm_bias_alpha_beta(ctx):
+    dtype = po.FP8E4M3
+    m, k, n = 64, 256, 96
+    a, sa, w_nk, w_src, sw, s_out = _linear_case(11, dtype, m, k, n, 1)
+    bias_f = rng(12).standard_normal(n).astype(np.float32) * 0.1
+    bias, sb = fp8_tensor(bias_f, dtype)
+    wt = ctx.prepare_weight(dev(w_src), dtype, k, n, 1, version=4)
+    for mm in (m, 8):
+        out = torch.empty((mm, n), dtype=torch.uint8, device="cuda")
+        ctx.fp8_linear(dev(a[:mm]), dtype, sa, mm, wt, sw, out, dtype, s_out, bias=dev(bias), bias_scale=sb,
+                       bias_kind=po.BIAS_VECTOR, alpha=0.5, beta=2.0)
+        ref = po.fp8_gemm(dtype, a[:mm], sa, w_nk, sw, True, s_out, bias=bias, s_bias=sb, bias_kind=po.BIAS_VECTOR,
+                          alpha=0.5, beta=2.0)
+        assert fp8_code_distance(host(out), ref).max() <= 1  # |sums| >> bias: no near-zero cancellation
+    wt.release()
+
+
+def test_fp8_linear_rejects_bad_scale(ctx):
+    dtype = po.FP8E4M3
+    a, sa, w_nk, w_src, sw, s_out = _linear_case(13, dtype, 2, 64, 32, 1)
+    wt = ctx.prepare_weight(dev(w_src), dtype, 64, 32, 1, version=5)
+    out = torch.empty((2, 32), dtype=torch.uint8, device="cuda")
+    rc = ctx.fp8_linear(dev(a), dtype, float("nan"), 2, wt, sw, out, dtype, s_out, check=False)
+    assert rc == -1
+    rc = ctx.fp8_linear(dev(a), dtype, sa, 2, wt, sw, out, dtype, 0.0, check=False)
+    assert rc == -1
+    wt.release()

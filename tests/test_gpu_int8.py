@@ -1,0 +1,169 @@
+"""GPU parity of the INT8 path (QuantizeLinear, MatMul/FC/Gemm INT8, Conv2D INT8, DequantizeLinear).
+
+Oracle: oracle/feather_oracle.c restating src/kernel/common/{gemm,fc,matmul,conv2d}.cc and
+quantize_linear_utils.h.  Bar: bit-exact int8/fp32 outputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import pyoracle as po
+from tests.common import SEEDS, rng
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a).cuda()
+
+
+def c1_inputs(seed=SEEDS[1], m=128, k=1024, n=1024):
+    """Config 1: X ~ N(0,1) per-tensor int8 (s = max|X|/127), W int8 U[-127,127] per-channel scales
+    U(1e-3, 1e-2), bias ~ N(0, 0.1) quantized as round(b / (s_x * s_w)) (static_quantizer.cc:256-287)."""
+    r = rng(seed)
+    x = r.standard_normal((m, k)).astype(np.float32)
+    s_x = np.float32(np.max(np.abs(x)) / 127.0)
+    w = r.integers(-127, 128, size=(n, k), dtype=np.int64).astype(np.int8)
+    s_w = r.uniform(1e-3, 1e-2, size=n).astype(np.float32)
+    b = (r.standard_normal(n) * 0.1).astype(np.float32)
+    bias = np.round(b.astype(np.float64) / (np.float64(s_x) * s_w.astype(np.float64))).astype(np.int32)
+    return x, s_x, w, s_w, bias
+
+
+def test_quantize_linear_fp32_per_tensor(ctx):
+    x, s_x, *_ = c1_inputs()
+    x = x.copy()
+    x[0, :8] = [np.nan, np.inf, -np.inf, 0.5 * s_x, -0.5 * s_x, 1.5 * s_x, 1e30, -1e30]
+    for zp in (0, 3, -128):
+        out = torch.empty(x.shape, dtype=torch.int8, device="cuda")
+        ctx.quantize_linear(dev(x), po.FP32, [s_x], [zp], out)
+        rc, ref = po.quantize_linear(po.FP32, x, [s_x], [zp])
+        assert rc == 0
+        assert np.array_equal(out.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("src_dtype", [po.BF16, po.FP16])
+def test_quantize_linear_half_per_channel(ctx, src_dtype):
+    r = rng(5)
+    x = r.standard_normal((4, 200, 3)).astype(np.float32)
+    bits = po.bf16_encode(x) if src_dtype == po.BF16 else po.fp16_encode(x)
+    scales = r.uniform(0.01, 0.05, 200).astype(np.float32)
+    zps = r.integers(-5, 6, 200).astype(np.int32)
+    out = torch.empty(x.shape, dtype=torch.int8, device="cuda")
+    ctx.quantize_linear(dev(bits), src_dtype, scales, zps, out, channels=200, inner=3)
+    rc, ref = po.quantize_linear(src_dtype, bits, scales, zps, axis=1)
+    assert rc == 0
+    assert np.array_equal(out.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("dst", [po.FP32, po.BF16, po.FP16])
+def test_dequantize_linear(ctx, dst):
+    q = np.arange(-128, 128, dtype=np.int8).reshape(16, 16)
+    q = np.tile(q, (3, 1))
+    for scales, zps, ch, inner, axis in (([0.0123], [7], 1, 1, -1), (list(np.linspace(0.01, 0.2, 16)), [1] * 16, 16, 1, 1)):
+        out = torch.empty(q.shape, dtype=torch.float32 if dst == po.FP32 else torch.int16, device="cuda")
+        ctx.dequantize_linear(dev(q), scales, zps, out, dst, channels=ch, inner=inner)
+        rc, ref = po.dequantize_linear(q, scales, zps, dst, axis=axis)
+        assert rc == 0
+        got = out.cpu().numpy()
+        if dst != po.FP32:
+            got = got.view(np.uint16)
+        assert np.array_equal(got.view(np.uint32) if dst == po.FP32 else got,
+                              ref.view(np.uint32) if dst == po.FP32 else ref)
+
+
+@pytest.mark.parametrize("kind", [po.I8_GEMM, po.I8_FC, po.I8_MATMUL])
+def test_i8_linear_config1_bitexact(ctx, kind):
+    x, s_x, w_nk, s_w, bias = c1_inputs()
+    m, k = x.shape
+    n = w_nk.shape[0]
+    _, xq = po.quantize_linear(po.FP32, x, [s_x], [0])
+    trans_b = kind == po.I8_GEMM
+    w_src = w_nk if trans_b else np.ascontiguousarray(w_nk.T)
+    bias_kind = po.BIAS_NONE if kind == po.I8_MATMUL else po.BIAS_VECTOR
+    # output scale from the fp32 reference (calibration rule max|y| / 127, tools/int8_calibrate.cc:146-147)
+    _, _, acc = po.i8_linear(kind, xq, s_x, 0, w_src, trans_b, s_w, None, bias, bias_kind, 1.0, 1.0, 1.0, 0, True)
+    y = (acc.astype(np.float64) + (bias if bias_kind else 0)) * s_x * s_w.astype(np.float64)
+    s_y = np.float32(np.max(np.abs(y)) / 127.0)
+    rc, ref, _ = po.i8_linear(kind, xq, s_x, 0, w_src, trans_b, s_w, None, bias, bias_kind, 1.0, 1.0, s_y, 0)
+    assert rc == 0
+    wt = ctx.prepare_weight(dev(w_src), po.INT8, k, n, 1 if trans_b else 0, scales=s_w, version=kind)
+    out = torch.empty((m, n), dtype=torch.int8, device="cuda")
+    ctx.i8_linear(kind, dev(xq), s_x, 0, m, wt, out, s_y, 0, bias=dev(bias), bias_kind=bias_kind,
+                  bias_abs_max=int(np.abs(bias).max()))
+    got = out.cpu().numpy()
+    assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatches"
+    wt.release()
+
+
+def test_i8_gemm_zero_points_alpha_beta_ragged(ctx):
+    r = rng(21)
+    m, k, n = 37, 80, 45
+    xq = r.integers(-128, 128, (m, k)).astype(np.int8)
+    w = r.integers(-127, 128, (n, k)).astype(np.int8)
+    s_w = np.float32(0.004)
+    bias = r.integers(-3000, 3000, (m, n)).astype(np.int32)
+    # power-of-two scales so exact .5 ties occur in the requantization
+    s_x, s_y = 0.0625, 2.0
+    for zp_a, zp_y, alpha, beta in ((5, -3, 1.0, 1.0), (-20, 10, 0.75, -1.5)):
+        rc, ref, _ = po.i8_linear(po.I8_GEMM, xq, s_x, zp_a, w, True, [s_w], None, bias, po.BIAS_MATRIX, alpha, beta,
+                                  s_y, zp_y)
+        assert rc == 0
+        wt = ctx.prepare_weight(dev(w), po.INT8, k, n, 1, scales=[s_w], version=9)
+        out = torch.empty((m, n), dtype=torch.int8, device="cuda")
+        ctx.i8_linear(po.I8_GEMM, dev(xq), s_x, zp_a, m, wt, out, s_y, zp_y, bias=dev(bias),
+                      bias_kind=po.BIAS_MATRIX, bias_abs_max=3000, alpha=alpha, beta=beta)
+        assert np.array_equal(out.cpu().numpy(), ref)
+        wt.release()
+
+
+def c4_inputs(seed=SEEDS[4], pow2=True):
+    r = rng(seed)
+    x = r.integers(-128, 128, (1, 64, 160, 160)).astype(np.int8)
+    w = r.integers(-127, 128, (128, 64, 3, 3)).astype(np.int8)
+    if pow2:
+        s_in = 0.0078125
+        s_w = (2.0 ** -r.integers(6, 9, 128)).astype(np.float32)
+    else:
+        s_in = np.float32(r.uniform(0.01, 0.02))
+        s_w = r.uniform(1e-3, 1e-2, 128).astype(np.float32)
+    bias = r.integers(-20000, 20000, 128).astype(np.int32)
+    return x, np.float32(s_in), w, s_w, bias
+
+
+@pytest.mark.parametrize("pow2", [True, False])
+def test_i8_conv_config4_bitexact(ctx, pow2):
+    x, s_in, w, s_w, bias = c4_inputs(pow2=pow2)
+    s_out = np.float32(0.25 if pow2 else 0.3)
+    rc, ref = po.i8_conv2d(x, s_in, 0, w, s_w, bias, 2, 1, s_out, 0)
+    assert rc == 0
+    wt = ctx.prepare_conv_weight(dev(w), s_w, version=4)
+    out = torch.empty(ref.shape, dtype=torch.int8, device="cuda")
+    ctx.i8_conv2d(dev(x), 0, s_in, 0, wt, out, s_out, 0, stride=(2, 2), pad=(1, 1), bias=dev(bias),
+                  bias_abs_max=20000)
+    got = out.cpu().numpy()
+    assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatches"
+    wt.release()
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+def test_i8_conv_groups_dilation_zero_point(ctx, layout):
+    r = rng(31)
+    n, c, h, wd, oc, g = 2, 8, 13, 11, 12, 2
+    x = r.integers(-128, 128, (n, c, h, wd)).astype(np.int8)
+    w = r.integers(-127, 128, (oc, c // g, 3, 2)).astype(np.int8)
+    s_w = r.uniform(1e-3, 1e-2, oc).astype(np.float32)
+    bias = r.integers(-500, 500, oc).astype(np.int32)
+    xl = x if layout == 0 else np.ascontiguousarray(x.transpose(0, 2, 3, 1))
+    rc, ref = po.i8_conv2d(xl, 0.05, -7, w, s_w, bias, (2, 1), (1, 2), 0.02, 4, dilation=(2, 1), group=g,
+                           layout=layout)
+    assert rc == 0
+    wt = ctx.prepare_conv_weight(dev(w), s_w, group=g, version=5)
+    out = torch.empty(ref.shape, dtype=torch.int8, device="cuda")
+    ctx.i8_conv2d(dev(xl), layout, 0.05, -7, wt, out, 0.02, 4, stride=(2, 1), pad=(1, 2), dilation=(2, 1),
+                  bias=dev(bias), bias_abs_max=500)
+    assert np.array_equal(out.cpu().numpy(), ref)
+    wt.release()
