@@ -1,0 +1,365 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized-linear hot path (BASELINE.json's metric, one GPU).
+
+Headline (`value`): config 2 of BASELINE.json -- FP8 e4m3 decode linear, M=1, K=1024, N=3584,
+bf16 activations in and bf16 out through the FP8 boundary (the exported Cast -> MatMul -> Cast
+chain, fused into one kernel) -- as HBM GB/s of algorithmic bytes.  One step = one call over one
+activation row.  80 weight copies (294 MB > the 256 MB MALL) are rotated so every step streams its
+weight from HBM.  Steps are captured once into a HIP graph through the library's own capture API
+(fhip_capture_*) and the graph is replayed; the timed region is bracketed by a device
+synchronisation on both sides.
+
+`roofline`: the dominant kernel's algorithmic bytes / its average duration from HIP event pairs
+around every launch, recorded on the kernel's stream during a separate eager pass.
+`cpu_baseline`: the reference's own x86 FP8 linear (oracle/_ref, built from the Feather sources)
+on the host, M=1 with its prepared (BF16-packed) weight, for a bounded ~10 s sample.
+`configs`: the other BASELINE.json configs (C1, C2 M=4/16, C3, C4, C5), same method.
+"""
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0
+INT8_PEAK_TOPS = 5000.0
+METRIC = "FP8/INT8 GEMM TOPS (% MFMA peak) + decode GEMV HBM GB/s (% peak), 1 GPU"
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=4000)
+    p.add_argument("--warmup", type=int, default=400)
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--only-headline", action="store_true")
+    p.add_argument("--no-cpu", action="store_true")
+    return p.parse_args()
+
+
+def fp8_pow2_scale(amax, e5):
+    maxf = 57344.0 if e5 else 448.0
+    return 1.0 if not amax > 0 else float(2.0 ** math.ceil(math.log2(amax / maxf)))
+
+
+class Bench:
+    def __init__(self, args):
+        import torch
+        from infer_amd import _lib as L
+        from infer_amd.runtime import Context
+        self.torch, self.L = torch, L
+        self.ctx = Context(0)
+        self.s = self.ctx.stream
+        self.gen = torch.Generator(device="cuda")
+        self.args = args
+
+    # -- data ---------------------------------------------------------------------------------
+    def randn(self, shape, seed, std=1.0):
+        self.gen.manual_seed(seed)
+        return self.torch.randn(shape, generator=self.gen, device="cuda", dtype=self.torch.float32) * std
+
+    def to_fp8(self, x, dtype):
+        """fp32 device tensor -> (codes, pow2 scale) with the library's own Cast."""
+        t = self.torch
+        s = fp8_pow2_scale(float(x.abs().max()), dtype == self.L.FP8E5M2)
+        codes = t.empty(x.shape, dtype=t.uint8, device="cuda")
+        self.ctx.cast(x, self.L.FP32, 1.0, codes, dtype, s)
+        return codes, s
+
+    def decode(self, codes, dtype, scale):
+        out = self.torch.empty(codes.shape, dtype=self.torch.float32, device="cuda")
+        self.ctx.cast(codes, dtype, scale, out, self.L.FP32, 1.0)
+        return out
+
+    # -- timing ---------------------------------------------------------------------------------
+    def graph_time(self, steps, reps, warm=3):
+        """steps: callables, each enqueues one step on ctx.stream.  Returns ms per step."""
+        t, ctx = self.torch, self.ctx
+        with t.cuda.stream(self.s):
+            for f in steps:  # eager warm-up grows workspaces before capture
+                f()
+            ctx.synchronize()
+            ctx.capture_begin()
+            for f in steps:
+                f()
+            g = ctx.capture_end()
+            for _ in range(warm):
+                ctx.graph_launch(g)
+            t.cuda.synchronize()
+            e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+            wall = time.perf_counter()
+            e0.record(self.s)
+            for _ in range(reps):
+                ctx.graph_launch(g)
+            e1.record(self.s)
+            t.cuda.synchronize()
+            wall = time.perf_counter() - wall
+        ctx.graph_destroy(g)
+        ms = e0.elapsed_time(e1)
+        return ms / (reps * len(steps)), wall
+
+    def kernel_time(self, step, n):
+        """Mean duration of one launch from event pairs around each launch (eager, same stream)."""
+        t = self.torch
+        evs = [(t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)) for _ in range(n)]
+        with t.cuda.stream(self.s):
+            step(0)
+            t.cuda.synchronize()
+            for i, (a, b) in enumerate(evs):
+                a.record(self.s)
+                step(i)
+                b.record(self.s)
+            t.cuda.synchronize()
+        d = [a.elapsed_time(b) for a, b in evs]
+        return statistics.mean(d), statistics.median(d)
+
+
+def headline(b, args):
+    t, L, ctx = b.torch, b.L, b.ctx
+    k, n, copies = 1024, 3584, 80
+    w = b.randn((k, n), 0xFEA70002, 0.02)                  # MatMul weight [K,N] (exporter layout)
+    w_codes, sw = b.to_fp8(w, L.FP8E4M3)
+    x = b.randn((1, k), 0xFEA70002 + 1)
+    xb = x.to(t.bfloat16)
+    s_in = fp8_pow2_scale(float(xb.float().abs().max()), False)
+    xc = t.empty((1, k), dtype=t.uint8, device="cuda")
+    ctx.cast(xb, L.BF16, 1.0, xc, L.FP8E4M3, s_in)
+    y = b.decode(xc, L.FP8E4M3, s_in) @ b.decode(w_codes, L.FP8E4M3, sw)
+    s_out = fp8_pow2_scale(float(y.abs().max()), False)
+    srcs = [w_codes.clone() for _ in range(copies)]
+    weights = [ctx.prepare_weight(s_, L.FP8E4M3, k, n, L.LAYOUT_KN, version=1) for s_ in srcs]
+    out = t.empty((1, n), dtype=t.bfloat16, device="cuda")
+
+    def step(i):
+        ctx.fp8_linear(xb, L.BF16, s_in, 1, weights[i % copies], sw, out, L.BF16, s_out)
+
+    ctx.synchronize()
+    backend = None
+    with t.cuda.stream(b.s):
+        step(0)
+        backend = ctx.last_backend()
+    for i in range(args.warmup):
+        step(i)
+    per_graph = 400
+    reps = max(1, args.steps // per_graph)
+    steps = [(lambda i=i: step(i)) for i in range(per_graph)]
+    ms, wall = b.graph_time(steps, reps)
+    kmean, kmed = b.kernel_time(step, 800)
+    bytes_step = k * n + k * 2 + n * 2
+    res = {
+        "ms_per_step": ms, "steps": reps * per_graph, "wall_s": wall, "bytes": bytes_step,
+        "value": bytes_step / (ms * 1e-3) / 1e9, "kernel_ms": kmean, "kernel_ms_median": kmed,
+        "backend": backend,
+    }
+    for wt in weights:
+        wt.release()
+    return res
+
+
+def cpu_headline(args):
+    """Reference x86 FP8 linear (prepared BF16-packed RHS), M=1, K=1024, N=3584, on host cores."""
+    import ctypes
+    import numpy as np
+    from oracle import pyoracle as po
+    if not po.ref_available():
+        return None
+    R = po.ref()
+    r = np.random.default_rng(0xFEA70002)
+    w = (r.standard_normal((1024, 3584), dtype=np.float32) * np.float32(0.02))
+    sw = fp8_pow2_scale(float(np.abs(w).max()), False)
+    wc = po.fp8_encode(po.FP8E4M3, w / np.float32(sw))
+    x = r.standard_normal((1, 1024), dtype=np.float32)
+    s_in = fp8_pow2_scale(float(np.abs(x).max()), False)
+    xc = po.fp8_encode(po.FP8E4M3, x / np.float32(s_in))
+    out = np.empty((1, 3584), np.uint8)
+    h = R.ref_fp8_packed_create(po.FP8E4M3, po._ptr(wc), 0, 1024, 3584)
+    times = []
+    t_end = time.perf_counter() + args.cpu_seconds
+    calls = 0
+    while time.perf_counter() < t_end or calls < 20:
+        t0 = time.perf_counter()
+        rc = R.ref_fp8_packed_compute(h, po._ptr(xc), s_in, sw, 1, po._ptr(out), 1.0)
+        times.append(time.perf_counter() - t0)
+        calls += 1
+        assert rc == 0
+    R.ref_fp8_packed_destroy(h)
+    med = statistics.median(times)
+    threads = min(4, R.ref_max_threads())
+    bytes_step = 1024 * 3584 + 1024 * 2 + 3584 * 2
+    return {
+        "value": bytes_step / med / 1e9, "unit": "GB/s", "cores": threads, "kind": "reference",
+        "sample": f"{calls} calls (~{args.cpu_seconds:.0f} s) of Feather x86 ComputeLinearRowMajorX86Fp8PackedRhs, "
+                  f"M=1 K=1024 N=3584 e4m3, median {med * 1e3:.3f} ms/call; the two memory-bound Cast nodes "
+                  f"(1024 + 3584 elements) are not included; host nproc={os.cpu_count()}",
+    }
+
+
+def extra_configs(b, args):
+    t, L, ctx = b.torch, b.L, b.ctx
+    res = {}
+
+    # C2 M=4, 16
+    k, n, copies = 1024, 3584, 80
+    w_codes, sw = b.to_fp8(b.randn((k, n), 0xFEA70002, 0.02), L.FP8E4M3)
+    srcs = [w_codes.clone() for _ in range(copies)]
+    weights = [ctx.prepare_weight(s_, L.FP8E4M3, k, n, L.LAYOUT_KN, version=2) for s_ in srcs]
+    for m in (4, 16):
+        xb = b.randn((m, k), 0xFEA70002 + m).to(t.bfloat16)
+        out = t.empty((m, n), dtype=t.bfloat16, device="cuda")
+
+        def step(i, xb=xb, out=out, m=m):
+            ctx.fp8_linear(xb, L.BF16, 0.0078125, m, weights[i % copies], sw, out, L.BF16, 0.03125)
+        ms, _ = b.graph_time([(lambda i=i: step(i)) for i in range(200)], 5)
+        km, _ = b.kernel_time(step, 200)
+        by = k * n + m * k * 2 + m * n * 2
+        res[f"C2_fp8_decode_M{m}"] = {"ms_per_step": ms, "GB/s": by / ms / 1e6, "kernel_ms": km,
+                                      "kernel_GB/s": by / km / 1e6, "hbm_frac": by / km / 1e6 / HBM_PEAK_GBS}
+    for wt in weights:
+        wt.release()
+    del srcs
+
+    # C3 FP8 e5m2 prefill: up-proj [4096,1024]x[1024->3584], down-proj [4096,3584]x[3584->1024]
+    m, k, n = 4096, 1024, 3584
+    E5 = L.FP8E5M2
+    a_codes, sa = b.to_fp8(b.randn((m, k), 0xFEA70003), E5)
+    wu_codes, su = b.to_fp8(b.randn((n, k), 0xFEA70003 + 1, 0.02), E5)
+    wd_codes, sd = b.to_fp8(b.randn((k, n), 0xFEA70003 + 2, 0.02), E5)
+    wu = ctx.prepare_weight(wu_codes, E5, k, n, L.LAYOUT_NK, version=3)
+    wd = ctx.prepare_weight(wd_codes, E5, n, k, L.LAYOUT_NK, version=3)
+    mid = t.empty((m, n), dtype=t.uint8, device="cuda")
+    out = t.empty((m, k), dtype=t.bfloat16, device="cuda")
+    s_mid, s_o = 0.125, 0.25
+
+    def up(i=0):
+        ctx.fp8_linear(a_codes, E5, sa, m, wu, su, mid, E5, s_mid)
+
+    def down(i=0):
+        ctx.fp8_linear(mid, E5, s_mid, m, wd, sd, out, L.BF16, s_o)
+    ms, _ = b.graph_time([up, down] * 10, 5)
+    ku, _ = b.kernel_time(up, 50)
+    kd, _ = b.kernel_time(down, 50)
+    fl = 2.0 * m * k * n
+    res["C3_fp8e5m2_prefill"] = {
+        "ms_per_gemm": ms, "TFLOP/s": fl / ms / 1e9, "mfma_frac": fl / ms / 1e9 / FP8_PEAK_TFLOPS,
+        "up_kernel_ms": ku, "up_TFLOP/s": fl / ku / 1e9, "down_kernel_ms": kd, "down_TFLOP/s": fl / kd / 1e9,
+        "backend": ctx.last_backend()}
+    wu.release()
+    wd.release()
+
+    # C1 INT8 linear chain: QuantizeLinear(fp32) -> Gemm INT8 (transB) -> DequantizeLinear(fp32)
+    m, k, n = 128, 1024, 1024
+    x = b.randn((m, k), 0xFEA70001)
+    s_x = float(x.abs().max()) / 127.0
+    b.gen.manual_seed(0xFEA70001 + 1)
+    wq = t.randint(-127, 128, (n, k), generator=b.gen, device="cuda", dtype=t.int8)
+    s_w = (t.rand(n, generator=b.gen, device="cuda") * 9e-3 + 1e-3).cpu().numpy()
+    bias = t.randint(-20000, 20000, (n,), generator=b.gen, device="cuda", dtype=t.int32)
+    w8 = ctx.prepare_weight(wq, L.INT8, k, n, L.LAYOUT_NK, scales=s_w, version=4)
+    xq = t.empty((m, k), dtype=t.int8, device="cuda")
+    yq = t.empty((m, n), dtype=t.int8, device="cuda")
+    y = t.empty((m, n), dtype=t.float32, device="cuda")
+    s_y = 0.05
+
+    def c1(i=0):
+        ctx.quantize_linear(x, L.FP32, [s_x], [0], xq)
+        ctx.i8_linear(L.I8_GEMM, xq, s_x, 0, m, w8, yq, s_y, 0, bias=bias, bias_kind=L.BIAS_VECTOR, bias_abs_max=20000)
+        ctx.dequantize_linear(yq, [s_y], [0], y, L.FP32)
+
+    def c1_gemm(i=0):
+        ctx.i8_linear(L.I8_GEMM, xq, s_x, 0, m, w8, yq, s_y, 0, bias=bias, bias_kind=L.BIAS_VECTOR, bias_abs_max=20000)
+    ms, _ = b.graph_time([c1] * 50, 10)
+    kg, _ = b.kernel_time(c1_gemm, 200)
+    ops = 2.0 * m * k * n
+    res["C1_int8_linear_chain"] = {"ms_per_step": ms, "TOPS": ops / ms / 1e9, "GB/s": 2101248 / ms / 1e6,
+                                   "gemm_kernel_ms": kg, "gemm_TOPS": ops / kg / 1e9,
+                                   "int8_frac": ops / kg / 1e9 / INT8_PEAK_TOPS}
+    w8.release()
+
+    # C4 INT8 conv 3x3 s2 p1 [1,64,160,160] -> [1,128,80,80]
+    b.gen.manual_seed(0xFEA70004)
+    xin = t.randint(-128, 128, (1, 64, 160, 160), generator=b.gen, device="cuda", dtype=t.int8)
+    wc = t.randint(-127, 128, (128, 64, 3, 3), generator=b.gen, device="cuda", dtype=t.int8)
+    sc = (t.rand(128, generator=b.gen, device="cuda") * 9e-3 + 1e-3).cpu().numpy()
+    cb = t.randint(-20000, 20000, (128,), generator=b.gen, device="cuda", dtype=t.int32)
+    wcp = ctx.prepare_conv_weight(wc, sc, version=5)
+    yc = t.empty((1, 128, 80, 80), dtype=t.int8, device="cuda")
+
+    def c4(i=0):
+        ctx.i8_conv2d(xin, L.NCHW, 0.0078125, 0, wcp, yc, 0.25, 0, stride=(2, 2), pad=(1, 1), bias=cb,
+                      bias_abs_max=20000)
+    ms, _ = b.graph_time([c4] * 50, 10)
+    kc, _ = b.kernel_time(c4, 100)
+    ops = 943718400.0
+    res["C4_int8_conv3x3s2"] = {"ms_per_step": ms, "TOPS": ops / ms / 1e9, "GB/s": 2531840 / ms / 1e6,
+                                "kernel_ms": kc, "int8_frac": ops / kc / 1e9 / INT8_PEAK_TOPS,
+                                "hbm_frac": 2531840 / kc / 1e6 / HBM_PEAK_GBS}
+    wcp.release()
+
+    # C5 BF16 LM head + argmax, V=151936 (311 MB > MALL)
+    k, v = 1024, 151936
+    wh = (b.randn((v, k), 0xFEA70005, 0.02)).to(t.bfloat16)
+    for m in (1, 8):
+        a = b.randn((m, k), 0xFEA70005 + m).to(t.bfloat16)
+        tok = t.empty(m, dtype=t.int64, device="cuda")
+
+        def c5(i=0, a=a, tok=tok):
+            ctx.bf16_gemv_argmax(a, wh, tok)
+        ms, _ = b.graph_time([c5] * 20, 10)
+        km, _ = b.kernel_time(c5, 50)
+        by = v * k * 2 + m * k * 2 + m * 8
+        res[f"C5_bf16_argmax_M{m}"] = {"ms_per_step": ms, "GB/s": by / ms / 1e6, "kernel_ms": km,
+                                       "hbm_frac": by / km / 1e6 / HBM_PEAK_GBS}
+    return res
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    b = Bench(args)
+    h = headline(b, args)
+    line = {
+        "metric": METRIC,
+        "value": round(h["value"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": h["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": h["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8e4m3 (fp32 accumulate)",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights, power-of-two FP8 scales)",
+        "config": {
+            "workload": "C2: FP8 e4m3 decode linear M=1 K=1024 N=3584, bf16 in -> Cast(fp8) -> MatMul -> "
+                        "Cast(bf16) fused in one kernel; 80 rotated weight copies (294 MB)",
+            "kernel": h["backend"], "graph_replayed": True,
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(h["bytes"] / h["kernel_ms"] / 1e6, 2), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(h["bytes"] / h["kernel_ms"] / 1e6 / HBM_PEAK_GBS, 4),
+            "traffic": None, "kernel_ms": h["kernel_ms"], "kernel_ms_median": h["kernel_ms_median"],
+        },
+        "cpu_baseline": None,
+    }
+    if not args.only_headline:
+        try:
+            line["configs"] = extra_configs(b, args)
+        except Exception as e:  # report, never hide, a failing extra config
+            line["configs_error"] = repr(e)
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_headline(args)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -22,6 +22,12 @@
 namespace {
 
 typedef float v2f __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 load_stream16(const uint8_t* p) {
+    const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(x.x, x.y, x.z, x.w);
+}
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
@@ -87,6 +93,40 @@ struct HeadParams {
     float* logits;    // optional [m][v]
 };
 
+// Transposing butterfly over the wave: v[0..V) holds V partial sums per lane (V a power of two
+// <= 64).  Each exchange step halves the values a lane keeps (the lane keeps the half selected by
+// its lane bit and adds its partner's copy of that half), so after log2(V) steps lane l owns the
+// wave-wide sum of value index  l >> (6 - log2 V), and the remaining steps are plain
+// butterflies.  V-1 + (6 - log2 V) shuffles in total instead of 6*V.
+template <int V>
+__device__ __forceinline__ float transpose_reduce(float (&v)[V], int lane) {
+    int cnt = V;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        if (cnt > 1) {
+            const int half = cnt / 2;
+            const bool upper = (lane & off) != 0;
+#pragma unroll
+            for (int i = 0; i < V / 2; ++i) {
+                if (i < half) {
+                    const float send = upper ? v[i] : v[i + half];
+                    const float keep = upper ? v[i + half] : v[i];
+                    v[i] = keep + __shfl_xor(send, off, 64);
+                }
+            }
+            cnt = half;
+        } else {
+            v[0] += __shfl_xor(v[0], off, 64);
+        }
+    }
+    return v[0];
+}
+
+template <int V>
+struct Log2 {
+    static constexpr int value = V <= 1 ? 0 : 1 + Log2<V / 2>::value;
+};
+
 template <int KIND, int MT, int kMaxT>
 __global__ __launch_bounds__(kThreads) void gemv_argmax_kernel(const uint8_t* __restrict__ a, int64_t m, int64_t k,
                                                                const uint8_t* __restrict__ w, int64_t v,
@@ -95,6 +135,8 @@ __global__ __launch_bounds__(kThreads) void gemv_argmax_kernel(const uint8_t* __
                                                                int64_t* __restrict__ tokens) {
     using H = Head<KIND>;
     constexpr int esize = KIND == 0 ? 2 : 1;
+    constexpr int V = kRows * MT;                 // values reduced per wave iteration
+    constexpr int kShift = 6 - Log2<V>::value;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int64_t row_bytes = k * esize;
@@ -109,84 +151,90 @@ __global__ __launch_bounds__(kThreads) void gemv_argmax_kernel(const uint8_t* __
             xa[j][t] = (j < m && c < chunks) ? *reinterpret_cast<const uint4*>(a + j * row_bytes + c * 16)
                                              : make_uint4(0, 0, 0, 0);
         }
+    // After the transposing reduction this lane owns value index my_idx = r * MT + j.
+    const int my_idx = lane >> kShift;
+    const int my_r = my_idx / MT, my_j = my_idx % MT;
+    const bool writer = (lane & ((1 << kShift) - 1)) == 0;
+    unsigned long long best = 0ull;
 
-    unsigned long long best[MT];
-#pragma unroll
-    for (int j = 0; j < MT; ++j) best[j] = 0ull;
-
-    const int64_t total_waves = (int64_t)gridDim.x * kWaves;
-    for (int64_t r0 = ((int64_t)blockIdx.x * kWaves + wave) * kRows; r0 < v; r0 += total_waves * kRows) {
-        float acc[kRows][MT];
-#pragma unroll
-        for (int r = 0; r < kRows; ++r)
-#pragma unroll
-            for (int j = 0; j < MT; ++j) acc[r][j] = 0.0f;
+    const int64_t stride = (int64_t)gridDim.x * kWaves * kRows;
+    // Register double buffer: the next strip of rows is requested before the current one is used.
+    uint4 wv[kMaxT][kRows], wn[kMaxT][kRows];
+    auto load_rows = [&](int64_t first, uint4 (&dst)[kMaxT][kRows]) {
 #pragma unroll
         for (int t = 0; t < kMaxT; ++t) {
             const int64_t c = lane + 64 * t;
             if (c < chunks) {
-                uint4 wv[kRows];
 #pragma unroll
                 for (int r = 0; r < kRows; ++r) {
-                    const int64_t row = r0 + r < v ? r0 + r : v - 1;
-                    wv[r] = *reinterpret_cast<const uint4*>(w + row * row_bytes + c * 16);
+                    const int64_t row = first + r < v ? first + r : v - 1;
+                    dst[t][r] = load_stream16(w + row * row_bytes + c * 16);
                 }
+            }
+        }
+    };
+    int64_t r0 = ((int64_t)blockIdx.x * kWaves + wave) * kRows;
+    if (r0 < v) load_rows(r0, wv);
+    for (; r0 < v; r0 += stride) {
+        if (r0 + stride < v) load_rows(r0 + stride, wn);
+        float acc[V];
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < kMaxT; ++t) {
+            const int64_t c = lane + 64 * t;
+            if (c < chunks) {
+                float wf[kRows][H::kPer16];
+#pragma unroll
+                for (int r = 0; r < kRows; ++r) H::decode(wv[t][r], wf[r]);
 #pragma unroll
                 for (int j = 0; j < MT; ++j) {
                     float xf[H::kPer16];
                     H::decode(xa[j][t], xf);
 #pragma unroll
                     for (int r = 0; r < kRows; ++r) {
-                        float wf[H::kPer16];
-                        H::decode(wv[r], wf);
-                        float s = acc[r][j];
+                        float s = acc[r * MT + j];
 #pragma unroll
-                        for (int i = 0; i < H::kPer16; ++i) s += xf[i] * wf[i];
-                        acc[r][j] = s;
+                        for (int i = 0; i < H::kPer16; ++i) s += xf[i] * wf[r][i];
+                        acc[r * MT + j] = s;
                     }
                 }
             }
         }
 #pragma unroll
-        for (int r = 0; r < kRows; ++r) {
+        for (int t = 0; t < kMaxT; ++t)
 #pragma unroll
-            for (int j = 0; j < MT; ++j) {
-                float s = acc[r][j];
-#pragma unroll
-                for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-                const int64_t row = r0 + r;
-                if (row < v && j < m) {
-                    uint16_t bf;
-                    if constexpr (KIND == 0) {
-                        bf = fhip::bf16_encode(s);
-                    } else {
-                        const uint8_t code = fhip::fp8_encode(s * hp.ab_scale / hp.out_scale, KIND == 2);
-                        s = fhip::fp8_decode(code, KIND == 2) * hp.out_scale;
-                        bf = fhip::bf16_encode(s);
-                    }
-                    const unsigned long long key = make_key(bf, row);
-                    best[j] = key > best[j] ? key : best[j];
-                    if (hp.logits != nullptr && lane == 0) hp.logits[j * v + row] = s;
-                }
+            for (int r = 0; r < kRows; ++r) wv[t][r] = wn[t][r];
+        float s = transpose_reduce<V>(acc, lane);
+        const int64_t row = r0 + my_r;
+        if (row < v && my_j < m) {
+            uint16_t bf;
+            if constexpr (KIND == 0) {
+                bf = fhip::bf16_encode(s);
+            } else {
+                const uint8_t code = fhip::fp8_encode(s * hp.ab_scale / hp.out_scale, KIND == 2);
+                s = fhip::fp8_decode(code, KIND == 2) * hp.out_scale;
+                bf = fhip::bf16_encode(s);
             }
+            const unsigned long long key = make_key(bf, row);
+            best = key > best ? key : best;
+            if (hp.logits != nullptr && writer) hp.logits[my_j * v + row] = s;
         }
     }
 
     // Block reduction -> partials[block][j]
-    __shared__ unsigned long long red[kWaves][MT];
-#pragma unroll
-    for (int j = 0; j < MT; ++j) {
-        const unsigned long long b = wave_max(best[j]);
-        if (lane == 0) red[wave][j] = b;
-    }
+    __shared__ unsigned long long red[kWaves * 64];
+    red[threadIdx.x] = best;
     __syncthreads();
     __shared__ bool last;
+    if (threadIdx.x < MT) {
+        unsigned long long b = 0ull;
+        for (int q = 0; q < kWaves * 64; ++q)
+            if (((q & 63) >> kShift) % MT == (int)threadIdx.x) b = red[q] > b ? red[q] : b;
+        partials[(int64_t)blockIdx.x * MT + threadIdx.x] = b;
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
-        for (int j = 0; j < MT; ++j) {
-            unsigned long long b = red[0][j];
-            for (int q = 1; q < kWaves; ++q) b = red[q][j] > b ? red[q][j] : b;
-            partials[(int64_t)blockIdx.x * MT + j] = b;
-        }
         __threadfence();
         const unsigned int ticket = atomicAdd(&scratch->done, 1u);
         last = ticket == gridDim.x - 1;
@@ -195,6 +243,7 @@ __global__ __launch_bounds__(kThreads) void gemv_argmax_kernel(const uint8_t* __
     if (!last) return;
     __threadfence();
     // Last block: reduce the partials of every block.
+    __shared__ unsigned long long fin[kWaves][MT];
     for (int j = 0; j < MT; ++j) {
         unsigned long long b = 0ull;
         for (int64_t q = threadIdx.x; q < gridDim.x; q += kThreads) {
@@ -202,13 +251,13 @@ __global__ __launch_bounds__(kThreads) void gemv_argmax_kernel(const uint8_t* __
             b = p > b ? p : b;
         }
         b = wave_max(b);
-        if (lane == 0) red[wave][j] = b;
+        if (lane == 0) fin[wave][j] = b;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
         for (int j = 0; j < MT && j < m; ++j) {
-            unsigned long long b = red[0][j];
-            for (int q = 1; q < kWaves; ++q) b = red[q][j] > b ? red[q][j] : b;
+            unsigned long long b = fin[0][j];
+            for (int q = 1; q < kWaves; ++q) b = fin[q][j] > b ? fin[q][j] : b;
             tokens[j] = key_index(b);
         }
         scratch->done = 0u;  // re-arm for the next call / graph replay
@@ -222,7 +271,10 @@ int launch(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k, const uint8
     (void)hipDeviceGetAttribute(&dev_cus, hipDeviceAttributeMultiprocessorCount, ctx->device);
     const int64_t rows_per_block = (int64_t)kWaves * kRows;
     int64_t grid = (v + rows_per_block - 1) / rows_per_block;
-    const int64_t cap = (int64_t)dev_cus * 8;  // persistent-ish: a few blocks per CU, grid-stride
+#ifndef FHIP_ARGMAX_BLOCKS_PER_CU
+#define FHIP_ARGMAX_BLOCKS_PER_CU 2
+#endif
+    const int64_t cap = (int64_t)dev_cus * FHIP_ARGMAX_BLOCKS_PER_CU;  // grid-stride over the vocabulary
     if (grid > cap) grid = cap;
     void* ws = nullptr;
     int rc = fhip::acquire_workspace(ctx, (size_t)grid * 16 * sizeof(unsigned long long), &ws);

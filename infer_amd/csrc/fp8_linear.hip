@@ -16,7 +16,10 @@
 //                          block scales, fp32 accumulation.
 // Weights come prepared as [Np][Kp] (K contiguous, zero padded; runtime.hip).
 #include "fhip_internal.h"
+
+#include <cmath>
 #include "codec.h"
+#include "wave.h"
 
 namespace {
 
@@ -24,6 +27,14 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v2f __attribute__((ext_vector_type(2)));
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (non-temporal: the weight is read once per call).
+__device__ __forceinline__ uint4 load_stream16(const uint8_t* p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 // Decodes four FP8 codes packed little-endian in `w` with the hardware OCP converters.
 template <bool E5>
@@ -49,6 +60,7 @@ struct Fp8Epilogue {
     float bias_scale;
     int bias_kind;
     float out_scale;
+    float out_inv;       // 1/out_scale when out_scale is a power of two, else 0 (divide)
     int out_dtype;       // FP8 (code), BF16 or FP32 (decoded through the FP8 code)
     void* out;
     int64_t n;           // row stride of out
@@ -63,7 +75,7 @@ struct Fp8Epilogue {
         } else {
             y *= alpha;
         }
-        const uint8_t code = fhip::fp8_encode(y / out_scale, e5);
+        const uint8_t code = fhip::fp8_encode(out_inv != 0.0f ? y * out_inv : y / out_scale, e5);
         const int64_t idx = row * n + col;
         if (out_dtype == FHIP_BF16) {
             static_cast<uint16_t*>(out)[idx] = fhip::bf16_encode(fhip::fp8_decode(code, e5) * out_scale);
@@ -75,53 +87,133 @@ struct Fp8Epilogue {
     }
 };
 
-// Loads activation element i of row r as an FP8 code: FP8 input is copied, BF16/FP32 input is
-// encoded with the preceding Cast node's rule Enc(x / a_scale).
-template <bool E5>
-__device__ __forceinline__ uint8_t activation_code(const void* a, int a_dtype, int64_t idx, float a_scale) {
-    if (a_dtype == FHIP_BF16) return fhip::fp8_encode(fhip::bf16_decode(static_cast<const uint16_t*>(a)[idx]) / a_scale, E5);
-    if (a_dtype == FHIP_FP32) return fhip::fp8_encode(static_cast<const float*>(a)[idx] / a_scale, E5);
-    return static_cast<const uint8_t*>(a)[idx];
+constexpr int kGemvThreads = 256;
+constexpr int kGemvMaxLds = 64 * 1024;
+#ifndef FHIP_GEMV_R1
+#define FHIP_GEMV_R1 2
+#endif
+
+// Activation staging: the block encodes its activation rows once into LDS as FP8 codes.  Every
+// thread takes groups of 4 elements (one 4/8/16-byte load for FP8/BF16/FP32) and issues all of its
+// loads before encoding any, so the staging costs one memory latency and a short encode chain.
+// `a_vec` = 1 when k % 4 == 0 and the rows are 16-byte aligned; otherwise a per-element path runs.
+// Scales: `inv` holds 1/s when s is a power of two (x * (1/s) is then exactly x / s, both being the
+// correctly rounded value of the same real number); otherwise inv = 0 and the kernel divides.
+template <int ADT>
+struct ActGroup {
+    static constexpr int kElems = 4;
+};
+
+__device__ __forceinline__ float scale_down(float x, float s, float inv) { return inv != 0.0f ? x * inv : x / s; }
+
+template <bool E5, int ADT>
+__device__ __forceinline__ uint8_t encode_act(uint32_t bits, float a_scale, float a_inv) {
+    const float x = ADT == 1 ? fhip::bits_f32(bits << 16) : fhip::bits_f32(bits);
+    return fhip::fp8_encode(scale_down(x, a_scale, a_inv), E5);
 }
 
-constexpr int kGemvThreads = 256;
-constexpr int kGemvRowsPerWave = 2;
-constexpr int kGemvMaxLds = 64 * 1024;
+template <bool E5, int ADT>
+__device__ __forceinline__ void stage_activations(const void* __restrict__ a, int a_vec, float a_scale, float a_inv,
+                                                  int64_t m, int64_t k, int64_t kp, int mt, uint8_t* xs, int tid) {
+    constexpr int kBatch = 4;
+    constexpr int esz = ADT == 0 ? 1 : (ADT == 1 ? 2 : 4);
+    const int64_t groups = (int64_t)mt * kp / 4;
+    const int64_t gpr = kp / 4;  // groups per row
+    if (a_vec) {
+        for (int64_t g0 = tid; g0 < groups; g0 += (int64_t)kGemvThreads * kBatch) {
+            uint32_t raw[kBatch][4];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const int64_t g = g0 + (int64_t)u * kGemvThreads;
+                const int64_t r = g / gpr, kk = (g - r * gpr) * 4;
+                raw[u][0] = raw[u][1] = raw[u][2] = raw[u][3] = 0u;
+                if (g < groups && r < m && kk < k) {
+                    const uint8_t* src = static_cast<const uint8_t*>(a) + (r * k + kk) * esz;
+                    if constexpr (ADT == 0) {
+                        raw[u][0] = *reinterpret_cast<const uint32_t*>(src);
+                    } else if constexpr (ADT == 1) {
+                        const uint2 v = *reinterpret_cast<const uint2*>(src);
+                        raw[u][0] = v.x & 0xffffu;
+                        raw[u][1] = v.x >> 16;
+                        raw[u][2] = v.y & 0xffffu;
+                        raw[u][3] = v.y >> 16;
+                    } else {
+                        const uint4 v = *reinterpret_cast<const uint4*>(src);
+                        raw[u][0] = v.x;
+                        raw[u][1] = v.y;
+                        raw[u][2] = v.z;
+                        raw[u][3] = v.w;
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const int64_t g = g0 + (int64_t)u * kGemvThreads;
+                if (g >= groups) continue;
+                uint32_t c;
+                if constexpr (ADT == 0) {
+                    c = raw[u][0];
+                } else {
+                    c = (uint32_t)encode_act<E5, ADT>(raw[u][0], a_scale, a_inv) |
+                        ((uint32_t)encode_act<E5, ADT>(raw[u][1], a_scale, a_inv) << 8) |
+                        ((uint32_t)encode_act<E5, ADT>(raw[u][2], a_scale, a_inv) << 16) |
+                        ((uint32_t)encode_act<E5, ADT>(raw[u][3], a_scale, a_inv) << 24);
+                }
+                *reinterpret_cast<uint32_t*>(xs + g * 4) = c;
+            }
+        }
+    } else {
+        for (int64_t idx = tid; idx < (int64_t)mt * kp; idx += kGemvThreads) {
+            const int64_t r = idx / kp, kk = idx - r * kp;
+            uint8_t code = 0;
+            if (r < m && kk < k) {
+                const int64_t e = r * k + kk;
+                if constexpr (ADT == 0) code = static_cast<const uint8_t*>(a)[e];
+                else if constexpr (ADT == 1) code = encode_act<E5, 1>(static_cast<const uint16_t*>(a)[e], a_scale, a_inv);
+                else code = encode_act<E5, 2>(fhip::f32_bits(static_cast<const float*>(a)[e]), a_scale, a_inv);
+            }
+            xs[idx] = code;
+        }
+    }
+}
 
 // grid.x = ceil(n / (4 waves * R rows)); one wave owns R weight rows, lane l owns the 16-byte
-// chunks l, l+64, ... of each row.
-template <bool E5, int MT>
-__global__ __launch_bounds__(kGemvThreads) void fp8_gemv_kernel(const void* __restrict__ a, int a_dtype, float a_scale,
+// chunks l, l+64, ... of each row.  The first chunk of every row is requested before the block
+// stages its activations, so the weight stream and the activation staging overlap (one HBM round
+// trip for K <= 1024 instead of two).
+template <bool E5, int MT, int R, int ADT>
+__global__ __launch_bounds__(kGemvThreads) void fp8_gemv_kernel(const void* __restrict__ a, int a_vec, float a_scale, float a_inv,
                                                                  int64_t m, int64_t k, const uint8_t* __restrict__ w,
                                                                  int64_t kp, int64_t n, Fp8Epilogue ep) {
     extern __shared__ __align__(16) uint8_t xs[];  // [MT][kp] FP8 codes
     const int tid = threadIdx.x;
-    for (int64_t idx = tid; idx < MT * kp; idx += kGemvThreads) {
-        const int64_t r = idx / kp, kk = idx - r * kp;
-        xs[idx] = (r < m && kk < k) ? activation_code<E5>(a, a_dtype, r * k + kk, a_scale) : (uint8_t)0;
-    }
-    __syncthreads();
-
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int64_t row0 = ((int64_t)blockIdx.x * (kGemvThreads / 64) + wave) * kGemvRowsPerWave;
-    float acc[kGemvRowsPerWave][MT];
+    const int64_t row0 = ((int64_t)blockIdx.x * (kGemvThreads / 64) + wave) * R;
+    const int64_t chunks = kp / 16;
+    // Rows past n stay inside the zero-padded prepared weight (Np is a multiple of 256).
+    uint4 wv[R];
+    if (lane < chunks) {
 #pragma unroll
-    for (int r = 0; r < kGemvRowsPerWave; ++r)
+        for (int r = 0; r < R; ++r) wv[r] = load_stream16(w + (row0 + r) * kp + lane * 16);
+    }
+    stage_activations<E5, ADT>(a, a_vec, a_scale, a_inv, m, k, kp, MT, xs, tid);
+    __syncthreads();
+
+    float acc[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int j = 0; j < MT; ++j) acc[r][j] = 0.0f;
 
-    const int64_t chunks = kp / 16;
     for (int64_t c = lane; c < chunks; c += 64) {
-        uint4 wv[kGemvRowsPerWave];
+        if (c != lane) {
 #pragma unroll
-        for (int r = 0; r < kGemvRowsPerWave; ++r) {
-            const int64_t row = row0 + r < n ? row0 + r : n - 1;  // clamp: duplicate work, never stored
-            wv[r] = *reinterpret_cast<const uint4*>(w + row * kp + c * 16);
+            for (int r = 0; r < R; ++r) wv[r] = load_stream16(w + (row0 + r) * kp + c * 16);
         }
-        float wf[kGemvRowsPerWave][16];
+        float wf[R][16];
 #pragma unroll
-        for (int r = 0; r < kGemvRowsPerWave; ++r) {
+        for (int r = 0; r < R; ++r) {
             decode4<E5>(wv[r].x, wf[r]);
             decode4<E5>(wv[r].y, wf[r] + 4);
             decode4<E5>(wv[r].z, wf[r] + 8);
@@ -136,7 +228,7 @@ __global__ __launch_bounds__(kGemvThreads) void fp8_gemv_kernel(const void* __re
             decode4<E5>(xv.z, xf + 8);
             decode4<E5>(xv.w, xf + 12);
 #pragma unroll
-            for (int r = 0; r < kGemvRowsPerWave; ++r) {
+            for (int r = 0; r < R; ++r) {
                 float s = acc[r][j];
 #pragma unroll
                 for (int i = 0; i < 16; ++i) s += wf[r][i] * xf[i];
@@ -146,16 +238,13 @@ __global__ __launch_bounds__(kGemvThreads) void fp8_gemv_kernel(const void* __re
     }
     // Butterfly over the 64 lanes: every lane ends with the full sums.
 #pragma unroll
-    for (int r = 0; r < kGemvRowsPerWave; ++r)
+    for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int j = 0; j < MT; ++j) {
-            float v = acc[r][j];
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-            acc[r][j] = v;
+            acc[r][j] = fhip::wave_sum(acc[r][j]);
         }
 #pragma unroll
-    for (int r = 0; r < kGemvRowsPerWave; ++r)
+    for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int j = 0; j < MT; ++j) {
             if (lane == r * MT + j && j < m && row0 + r < n) ep.store(acc[r][j], j, row0 + r);
@@ -255,6 +344,15 @@ __global__ void cast_kernel(const void* __restrict__ src, int src_dtype, float s
     }
 }
 
+// 1/s when s is a power of two (exact), else 0.
+float pow2_inverse(float s) {
+    int e = 0;
+    const float f = std::frexp(s, &e);
+    if (f != 0.5f) return 0.0f;
+    const float inv = std::ldexp(1.0f, 1 - e);
+    return std::isfinite(inv) && inv * s == 1.0f ? inv : 0.0f;
+}
+
 bool is_fp8(int d) { return d == FHIP_FP8E4M3 || d == FHIP_FP8E5M2; }
 bool is_castable(int d) { return d == FHIP_FP32 || d == FHIP_BF16 || d == FHIP_FP16 || is_fp8(d); }
 size_t dtype_bytes(int d) { return d == FHIP_FP32 ? 4 : (d == FHIP_BF16 || d == FHIP_FP16 ? 2 : 1); }
@@ -265,28 +363,39 @@ unsigned grid_for(int64_t count, int threads) {
     return (unsigned)(blocks < 1 ? 1 : blocks);
 }
 
+// Rows per wave: small m streams more rows per wave to keep more bytes in flight per lane.
+template <bool E5, int ADT>
+int launch_gemv_t(fhip_context ctx, const void* a, float a_scale, int64_t m, const fhip_weight_s* w,
+                  const Fp8Epilogue& ep) {
+    const int64_t kp = ((w->k + 127) / 128) * 128;
+    const uint8_t* wd = static_cast<const uint8_t*>(w->data);
+    const int a_vec = (w->k % 4 == 0 && (reinterpret_cast<uintptr_t>(a) & 15) == 0) ? 1 : 0;
+    const float a_inv = pow2_inverse(a_scale);
+#define FHIP_GEMV_CASE(MT, R)                                                                                       \
+    if (m <= MT) {                                                                                                  \
+        const unsigned grid = (unsigned)((w->n + 4 * R - 1) / (4 * R));                                             \
+        const size_t lds = (size_t)MT * kp;                                                                         \
+        fp8_gemv_kernel<E5, MT, R, ADT><<<grid, kGemvThreads, lds, ctx->stream>>>(a, a_vec, a_scale, a_inv, m, w->k, wd,   \
+                                                                                  kp, w->n, ep);                    \
+        ctx->last_backend = "fp8_gemv_m" #MT;                                                                      \
+        FHIP_CHECK_LAUNCH(ctx, "fp8_gemv_kernel");                                                                  \
+        return FHIP_OK;                                                                                             \
+    }
+    FHIP_GEMV_CASE(1, FHIP_GEMV_R1)
+    FHIP_GEMV_CASE(2, 2)
+    FHIP_GEMV_CASE(4, 2)
+    FHIP_GEMV_CASE(8, 2)
+    FHIP_GEMV_CASE(16, 2)
+#undef FHIP_GEMV_CASE
+    return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "gemv: m > 16");
+}
+
 template <bool E5>
 int launch_gemv(fhip_context ctx, const void* a, int a_dtype, float a_scale, int64_t m, const fhip_weight_s* w,
                 const Fp8Epilogue& ep) {
-    const int64_t kp = ((w->k + 127) / 128) * 128;
-    const unsigned grid = (unsigned)((w->n + 4 * kGemvRowsPerWave - 1) / (4 * kGemvRowsPerWave));
-    const uint8_t* wd = static_cast<const uint8_t*>(w->data);
-#define FHIP_GEMV_CASE(MT)                                                                                      \
-    if (m <= MT) {                                                                                              \
-        const size_t lds = (size_t)MT * kp;                                                                     \
-        fp8_gemv_kernel<E5, MT><<<grid, kGemvThreads, lds, ctx->stream>>>(a, a_dtype, a_scale, m, w->k, wd, kp, \
-                                                                          w->n, ep);                            \
-        ctx->last_backend = "fp8_gemv_m" #MT;                                                                  \
-        FHIP_CHECK_LAUNCH(ctx, "fp8_gemv_kernel");                                                              \
-        return FHIP_OK;                                                                                         \
-    }
-    FHIP_GEMV_CASE(1)
-    FHIP_GEMV_CASE(2)
-    FHIP_GEMV_CASE(4)
-    FHIP_GEMV_CASE(8)
-    FHIP_GEMV_CASE(16)
-#undef FHIP_GEMV_CASE
-    return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "gemv: m > 16");
+    if (a_dtype == FHIP_BF16) return launch_gemv_t<E5, 1>(ctx, a, a_scale, m, w, ep);
+    if (a_dtype == FHIP_FP32) return launch_gemv_t<E5, 2>(ctx, a, a_scale, m, w, ep);
+    return launch_gemv_t<E5, 0>(ctx, a, a_scale, m, w, ep);
 }
 
 template <bool E5>
@@ -335,7 +444,8 @@ int fhip_fp8_linear(fhip_context ctx, int a_dtype, const void* a, float a_scale,
         bias_kind < FHIP_BIAS_NONE || bias_kind > FHIP_BIAS_MATRIX)
         return fhip::set_error(ctx, FHIP_ERR_INVALID, "fp8_linear: scales must be finite and positive");
     const bool e5 = w->dtype == FHIP_FP8E5M2;
-    Fp8Epilogue ep{a_scale * w_scale, alpha, beta, bias, bias_scale, bias_kind, out_scale, out_dtype, out, w->n, e5};
+    Fp8Epilogue ep{a_scale * w_scale, alpha, beta, bias, bias_scale, bias_kind, out_scale, pow2_inverse(out_scale),
+                   out_dtype, out, w->n, e5};
     const int64_t kp = ((w->k + 127) / 128) * 128;
     if (m <= 16 && (size_t)(16 * kp) <= (size_t)kGemvMaxLds) {
         return e5 ? launch_gemv<true>(ctx, a, a_dtype, a_scale, m, w, ep)
