@@ -1,0 +1,104 @@
+// fp8_common.h -- pieces shared by the FP8 GEMV and GEMM kernels: operand decode, streaming loads
+// and the output epilogue (the reference's alpha/beta/bias/out_scale rule and the FP8 output code).
+#ifndef FHIP_FP8_COMMON_H
+#define FHIP_FP8_COMMON_H
+
+#include "fhip_internal.h"
+#include "codec.h"
+
+namespace fhip {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (non-temporal: the weight is read once per call).
+__device__ __forceinline__ uint4 load_stream16(const uint8_t* p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Decodes four FP8 codes packed little-endian in `w` with the hardware OCP converters.
+template <bool E5>
+__device__ __forceinline__ void decode4(uint32_t w, float* out) {
+    v2f lo, hi;
+    if constexpr (E5) {
+        lo = __builtin_amdgcn_cvt_pk_f32_bf8((int)w, false);
+        hi = __builtin_amdgcn_cvt_pk_f32_bf8((int)w, true);
+    } else {
+        lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+        hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+    }
+    out[0] = lo.x;
+    out[1] = lo.y;
+    out[2] = hi.x;
+    out[3] = hi.y;
+}
+
+struct Fp8Epilogue {
+    float ab_scale;      // a_scale * w_scale
+    float alpha, beta;
+    const uint8_t* bias;
+    float bias_scale;
+    int bias_kind;
+    float out_scale;
+    float out_inv;       // 1/out_scale when out_scale is a power of two, else 0 (divide)
+    int out_dtype;       // FP8 (code), BF16 or FP32 (decoded through the FP8 code)
+    void* out;
+    int64_t n;           // row stride of out
+    bool e5;
+
+    // Output element bits (FP8 code, BF16 bits or FP32 bits) for accumulator `acc` at (row, col).
+    __device__ __forceinline__ uint32_t value(float acc, int64_t row, int64_t col) const {
+        float y = acc * ab_scale;
+        y *= alpha;
+        if (bias_kind != FHIP_BIAS_NONE) {
+            const uint8_t bc = bias[bias_kind == FHIP_BIAS_VECTOR ? col : row * n + col];
+            y += beta * (fhip::fp8_decode(bc, e5) * bias_scale);
+        }
+        const uint8_t code = fhip::fp8_encode(out_inv != 0.0f ? y * out_inv : y / out_scale, e5);
+        if (out_dtype == FHIP_BF16) return fhip::bf16_encode(fhip::fp8_decode(code, e5) * out_scale);
+        if (out_dtype == FHIP_FP32) return fhip::f32_bits(fhip::fp8_decode(code, e5) * out_scale);
+        return code;
+    }
+
+    __device__ __forceinline__ void store(float acc, int64_t row, int64_t col) const {
+        float y = acc * ab_scale;
+        if (bias_kind != FHIP_BIAS_NONE) {
+            y *= alpha;
+            const uint8_t bc = bias[bias_kind == FHIP_BIAS_VECTOR ? col : row * n + col];
+            y += beta * (fhip::fp8_decode(bc, e5) * bias_scale);
+        } else {
+            y *= alpha;
+        }
+        const uint8_t code = fhip::fp8_encode(out_inv != 0.0f ? y * out_inv : y / out_scale, e5);
+        const int64_t idx = row * n + col;
+        if (out_dtype == FHIP_BF16) {
+            static_cast<uint16_t*>(out)[idx] = fhip::bf16_encode(fhip::fp8_decode(code, e5) * out_scale);
+        } else if (out_dtype == FHIP_FP32) {
+            static_cast<float*>(out)[idx] = fhip::fp8_decode(code, e5) * out_scale;
+        } else {
+            static_cast<uint8_t*>(out)[idx] = code;
+        }
+    }
+};
+
+constexpr int kGemvThreads = 256;
+constexpr int kGemvMaxLds = 64 * 1024;
+#ifndef FHIP_GEMV_R1
+#define FHIP_GEMV_R1 2
+#endif
+
+
+// 1/s when s is a power of two (x * (1/s) then equals x / s exactly), else 0.
+float pow2_inverse(float s);
+
+// a: FP8 codes [m][k64], k64 % 64 == 0, 16-byte aligned rows; k64 <= the weight's padded K.
+int launch_fp8_gemm(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, const fhip_weight_s* w,
+                    const Fp8Epilogue& ep);
+
+}  // namespace fhip
+
+#endif  // FHIP_FP8_COMMON_H

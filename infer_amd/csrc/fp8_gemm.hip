@@ -1,0 +1,396 @@
+// fp8_gemm.hip -- FP8 (e4m3 / e5m2) prefill GEMM on gfx950 MFMA.
+//
+// out[m, n] = epilogue( sum_k Dec(A[m,k]) * Dec(B[n,k]) )   (Fp8Epilogue: scales, alpha/beta/bias,
+// FP8 output code, optional decode to BF16/FP32 -- src/kernel/common/gemm.cc:62-100).
+//
+// Tiling:
+//   * block tile BM x BN, 4 waves (256 threads) arranged WAVES_M x WAVES_N; K advances 64 per stage;
+//   * v_mfma_scale_f32_32x32x64_f8f6f4 with unit block scales (scale exponent 127), fp32 accumulators;
+//     lane l supplies row/column l%32 and the 32-byte K slice (l/32) of the 64-deep stage, for A and
+//     B alike, so both index the same K in every MFMA slot;
+//   * A (activations, [m][k]) and B (prepared weight, [Np][Kp]) stages live in LDS with an 80-byte row
+//     pitch: the 16 lanes of a ds_read_b128 group hit 16 distinct 4-bank groups (5*r mod 16 distinct);
+//   * two LDS stages: the global loads of stage s+1 are in flight while stage s feeds the MFMAs;
+//   * tile order is XCD-aware: consecutive workgroups land on different XCDs (round-robin dispatch),
+//     so the tile index is re-derived to give each XCD a contiguous block of tiles (shared operand rows
+//     stay in that XCD's L2);
+//   * epilogue: accumulators -> output bits -> LDS tile -> coalesced 16-byte global stores.
+#include "fp8_common.h"
+
+#include <utility>
+
+namespace {
+
+using namespace fhip;
+
+constexpr int kBK = 64;
+constexpr int kStages = 4;
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [0, N).  Used where the accumulator
+// registers are indexed, so no index is ever a runtime value (which would demote them to scratch).
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// LDS stage: A rows [BM][64 B], then B rows [BNP][64 B] (BNP = BN rounded up to 64 rows so every
+// wave issues the same number of 16-byte loads).  Rows are unpadded; the 16-byte chunk c of row r
+// sits at position c ^ swz(r), swz(r) = (r >> 2) & 3, which keeps the 16 lanes of every
+// ds_read_b128 group on 16 distinct 4-bank groups.
+template <int BM, int BN>
+struct Stage {
+    static constexpr int BNP = (BN + 63) / 64 * 64;
+    static constexpr int kA = BM * kBK;
+    static constexpr int kBytes = (BM + BNP) * kBK;
+    static constexpr int kLoadsA = BM * 4 / 256;   // 16-byte loads per thread per stage
+    static constexpr int kLoadsB = BNP * 4 / 256;
+    static constexpr int kLoads = kLoadsA + kLoadsB;
+};
+
+__device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+__device__ __forceinline__ void load_to_lds(const uint8_t* g, uint8_t* lds_wave_base) {
+    __builtin_amdgcn_global_load_lds(static_cast<const void*>(g), (lds_ptr)(lds_wave_base), 16, 0, 0);
+}
+
+// LDS fragment read issued as inline asm.  The compiler's wait-count pass treats every LDS read as
+// possibly aliasing the in-flight LDS-DMA stage loads and would put a vmcnt(0) in front of it, draining
+// the whole load pipeline each stage; the explicit vmcnt(N) + s_barrier above each stage already
+// orders these reads.  The matching lgkmcnt wait is lds_fence() below.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4_t lds_read16(const uint8_t* p) {
+    u32x4_t v;
+    const unsigned addr = (unsigned)(uintptr_t)(lds_ptr)(p);
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+
+template <int FM, int FN>
+__device__ __forceinline__ void lds_fence(u32x4_t (&fa)[FM][2], u32x4_t (&fb)[FN][2]) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < FM; ++i) asm volatile("" : "+v"(fa[i][0]), "+v"(fa[i][1]));
+#pragma unroll
+    for (int j = 0; j < FN; ++j) asm volatile("" : "+v"(fb[j][0]), "+v"(fb[j][1]));
+}
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | (((N >> 4) & 3) << 14));
+}
+
+// Output bits for one accumulator, branch-free.  The hardware converter encodes finite in-range values
+// (round to nearest even; checked against the reference codec on every such input by the GPU test
+// suite); values beyond the largest finite code are replaced with the reference's saturated / special
+// codes by selects: finite overflow -> max finite, Inf -> 0x7e (e4m3) / 0x7c (e5m2), NaN -> 0x7f / 0x7d,
+// each with the value's sign (include/util/fp8.h:66-211).
+// y / out_scale for one accumulator.  Without a bias the whole chain acc*ab_scale*alpha/out_scale is one
+// multiply by a precombined factor when out_scale is a power of two (`mul`); with a bias it follows the
+// reference's order: alpha*sum + beta*bias, then the division by out_scale (gemm.cc:87-98).
+template <bool E5, bool POW2, bool BIAS>
+__device__ __forceinline__ float scaled(const Fp8Epilogue& ep, float mul, float acc, int64_t row, int64_t col) {
+    if constexpr (!BIAS) {
+        if constexpr (POW2) return acc * mul;
+        return (acc * ep.ab_scale * ep.alpha) / ep.out_scale;
+    } else {
+        float y = acc * ep.ab_scale * ep.alpha;
+        const uint8_t bc = ep.bias[ep.bias_kind == FHIP_BIAS_VECTOR ? col : row * ep.n + col];
+        y += ep.beta * (fhip::fp8_decode(bc, E5) * ep.bias_scale);
+        return POW2 ? y * ep.out_inv : y / ep.out_scale;
+    }
+}
+
+template <bool E5>
+__device__ __forceinline__ uint32_t fixup_code(float q, uint32_t hw_code) {
+    const uint32_t bits = __float_as_uint(q);
+    const uint32_t mag = bits & 0x7fffffffu;
+    const uint32_t sign = (bits >> 24) & 0x80u;
+    const uint32_t special = mag > 0x7f800000u ? (E5 ? 0x7du : 0x7fu)
+                                                : (mag == 0x7f800000u ? (E5 ? 0x7cu : 0x7eu) : (E5 ? 0x7bu : 0x7eu));
+    return mag <= (E5 ? 0x47600000u : 0x43e00000u) ? hw_code : (sign | special);
+}
+
+template <bool E5>
+__device__ __forceinline__ float decode_code(uint32_t code) {
+    const v2f d = E5 ? __builtin_amdgcn_cvt_pk_f32_bf8((int)code, false) : __builtin_amdgcn_cvt_pk_f32_fp8((int)code, false);
+    return (d.x != d.x) ? __uint_as_float(0x7fc00000u) : d.x;  // the reference decodes NaN codes to +qNaN
+}
+
+// Output bits of four consecutive columns (col..col+3) of one row, packed little-endian: four FP8 codes
+// in one dword (OUT_BYTES 1), four BF16 in two dwords (2) or four FP32 (4).  The hardware converter
+// encodes finite in-range values (round to nearest even; checked against the reference codec on every
+// such input by the GPU test suite); beyond the largest finite code the reference's saturated and
+// special codes are selected instead: finite overflow -> max finite, Inf -> 0x7e (e4m3) / 0x7c (e5m2),
+// NaN -> 0x7f / 0x7d, each with the value's sign (include/util/fp8.h:66-211).
+template <bool E5, bool POW2, bool BIAS, int OUT_BYTES>
+__device__ __forceinline__ void fast_value4(const Fp8Epilogue& ep, float mul, const float (&acc)[4], int64_t row,
+                                            int64_t col, uint32_t (&out)[OUT_BYTES]) {
+    float q[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) q[t] = scaled<E5, POW2, BIAS>(ep, mul, acc[t], row, col + t);
+    int pk = E5 ? __builtin_amdgcn_cvt_pk_bf8_f32(q[0], q[1], 0, false) : __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+    pk = E5 ? __builtin_amdgcn_cvt_pk_bf8_f32(q[2], q[3], pk, true) : __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], pk, true);
+    const float maxf = E5 ? 57344.0f : 448.0f;
+    uint32_t packed = (uint32_t)pk;
+    // NaN fails every comparison, so it also takes the fix-up path.
+    const bool in_range = __builtin_fabsf(q[0]) <= maxf && __builtin_fabsf(q[1]) <= maxf &&
+                          __builtin_fabsf(q[2]) <= maxf && __builtin_fabsf(q[3]) <= maxf;
+    if (__builtin_expect(!in_range, 0)) {
+        packed = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) packed |= fixup_code<E5>(q[t], ((uint32_t)pk >> (8 * t)) & 0xffu) << (8 * t);
+    }
+    if constexpr (OUT_BYTES == 1) {
+        out[0] = packed;
+    } else {
+        float v[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] = decode_code<E5>((packed >> (8 * t)) & 0xffu) * ep.out_scale;
+        if constexpr (OUT_BYTES == 2) {
+            out[0] = (uint32_t)fhip::bf16_encode(v[0]) | ((uint32_t)fhip::bf16_encode(v[1]) << 16);
+            out[1] = (uint32_t)fhip::bf16_encode(v[2]) | ((uint32_t)fhip::bf16_encode(v[3]) << 16);
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) out[t] = __float_as_uint(v[t]);
+        }
+    }
+}
+
+template <bool E5, int BM, int BN, int WAVES_M, int WAVES_N, int OUT_BYTES, bool POW2>
+__global__ __launch_bounds__(256) void fp8_gemm_kernel(const uint8_t* __restrict__ a, int64_t m, int64_t k,
+                                                       const uint8_t* __restrict__ b, int64_t kp, int64_t np,
+                                                       int tiles_n, int tiles_total, Fp8Epilogue ep) {
+    using S = Stage<BM, BN>;
+    constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
+    constexpr int FM = WTM / 32, FN = WTN / 32;
+    static_assert(FM * 32 == WTM && FN * 32 == WTN, "wave tile must be a multiple of 32");
+    constexpr int fmt = E5 ? 1 : 0;
+    extern __shared__ __align__(16) uint8_t smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+
+    int tile = blockIdx.x;
+    const int nb = gridDim.x;
+    if ((nb & 7) == 0) tile = (tile & 7) * (nb >> 3) + (tile >> 3);
+    if (tile >= tiles_total) return;
+    const int64_t m0 = (int64_t)(tile / tiles_n) * BM;
+    const int64_t n0 = (int64_t)(tile % tiles_n) * BN;
+
+    // Per-thread source rows and chunks of its 16-byte loads (fixed for the whole K loop).
+    const uint8_t* src[S::kLoads];
+#pragma unroll
+    for (int i = 0; i < S::kLoads; ++i) {
+        const bool is_a = i < S::kLoadsA;
+        const int q = (is_a ? i : i - S::kLoadsA) * 256 + tid;
+        const int r = q >> 2;
+        const int c = (q & 3) ^ swz(r);
+        if (is_a) {
+            const int64_t row = m0 + r < m ? m0 + r : m - 1;   // rows past m are computed, never stored
+            src[i] = a + row * k + c * 16;
+        } else {
+            const int64_t row = n0 + r < np ? n0 + r : np - 1;
+            src[i] = b + row * kp + c * 16;
+        }
+    }
+    auto issue = [&](int kt) {
+        uint8_t* st = smem + (kt % kStages) * S::kBytes;
+#pragma unroll
+        for (int i = 0; i < S::kLoads; ++i) {
+            const bool is_a = i < S::kLoadsA;
+            const int slot = is_a ? i : i - S::kLoadsA;
+            uint8_t* dst = st + (is_a ? 0 : S::kA) + (slot * 256 + wave * 64) * 16;
+            load_to_lds(src[i] + (int64_t)kt * kBK, dst);
+        }
+    };
+
+    v16f acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    const int nk = (int)(k / kBK);  // host guarantees k % 64 == 0
+#pragma unroll
+    for (int s0 = 0; s0 < kStages - 1; ++s0)
+        if (s0 < nk) issue(s0);
+
+    const int frag_row = lane & 31;
+    const int frag_c = (lane >> 5) * 2;
+    for (int kt = 0; kt < nk; ++kt) {
+        const int ahead = nk - 1 - kt;  // stages issued after kt (capped below)
+        if (ahead >= 2) wait_vmcnt<2 * S::kLoads>();
+        else if (ahead == 1) wait_vmcnt<S::kLoads>();
+        else wait_vmcnt<0>();
+        // Plain s_barrier: the explicit vmcnt wait above already covers this wave's stage loads, and a
+        // __syncthreads() fence would also wait for the loads of the stages still in flight.
+        __builtin_amdgcn_s_barrier();
+#ifndef FHIP_GEMM_PROBE_NOLOAD
+        if (kt + kStages - 1 < nk) issue(kt + kStages - 1);
+#endif
+        const uint8_t* sa = smem + (kt % kStages) * S::kBytes;
+        const uint8_t* sb = sa + S::kA;
+        u32x4_t fa[FM][2], fb[FN][2];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const int r = wm * WTM + i * 32 + frag_row;
+            const uint8_t* row = sa + r * kBK;
+            fa[i][0] = lds_read16(row + ((frag_c ^ swz(r)) << 4));
+            fa[i][1] = lds_read16(row + (((frag_c + 1) ^ swz(r)) << 4));
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int r = wn * WTN + j * 32 + frag_row;
+            const uint8_t* row = sb + r * kBK;
+            fb[j][0] = lds_read16(row + ((frag_c ^ swz(r)) << 4));
+            fb[j][1] = lds_read16(row + (((frag_c + 1) ^ swz(r)) << 4));
+        }
+        // Wait for the fragment reads; every fragment register is an operand, so no MFMA that uses one
+        // can be scheduled above the wait.
+        lds_fence<FM, FN>(fa, fb);
+        v8i af[FM], bf[FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+            af[i] = v8i{(int)fa[i][0].x, (int)fa[i][0].y, (int)fa[i][0].z, (int)fa[i][0].w,
+                        (int)fa[i][1].x, (int)fa[i][1].y, (int)fa[i][1].z, (int)fa[i][1].w};
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+            bf[j] = v8i{(int)fb[j][0].x, (int)fb[j][0].y, (int)fb[j][0].z, (int)fb[j][0].w,
+                        (int)fb[j][1].x, (int)fb[j][1].y, (int)fb[j][1].z, (int)fb[j][1].w};
+#ifndef FHIP_GEMM_PROBE_NOMFMA
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af[i], acc[i][j], fmt, fmt, 0, 127,
+                                                                            0, 127);
+#endif
+    }
+    __syncthreads();
+#ifdef FHIP_GEMM_PROBE_NOEPI
+    {
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) t += acc[i][j][e];
+        if (t == 12345.0f) static_cast<uint8_t*>(ep.out)[tid] = 1;
+        return;
+    }
+#endif
+
+    // ---- epilogue.  The MFMA computed each 32x32 block transposed (weight fragment as the row operand),
+    // so lane l holds output row m = l%32 of the block and, for e = 4g..4g+3, the four consecutive
+    // output columns 8g + 4*(l/32) .. +3: one packed dword (FP8) per group, staged in an LDS tile and
+    // written out with coalesced 16-byte stores.
+    constexpr int kOutPitch = BN * OUT_BYTES + 16;
+    uint8_t* so = smem;
+    const int row_in = lane & 31;
+    const int col_q = (lane >> 5) * 4;
+    const float mul = ep.ab_scale * ep.alpha * ep.out_inv;
+    auto epilogue = [&](auto bias_tag) {
+        constexpr bool BIAS = decltype(bias_tag)::value;
+        static_for<FM * FN>([&](auto ij) {
+            constexpr int i = decltype(ij)::value / FN, j = decltype(ij)::value % FN;
+            static_for<4>([&](auto gg) {
+                constexpr int g = decltype(gg)::value;
+                const int r = wm * WTM + i * 32 + row_in;
+                const int c = wn * WTN + j * 32 + g * 8 + col_q;
+                const float v4[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+                uint32_t packed[OUT_BYTES];
+                fast_value4<E5, POW2, BIAS, OUT_BYTES>(ep, mul, v4, m0 + r, n0 + c, packed);
+                uint8_t* dst = so + r * kOutPitch + c * OUT_BYTES;
+                if constexpr (OUT_BYTES == 1) *reinterpret_cast<uint32_t*>(dst) = packed[0];
+                else if constexpr (OUT_BYTES == 2) *reinterpret_cast<uint2*>(dst) = make_uint2(packed[0], packed[1]);
+                else *reinterpret_cast<uint4*>(dst) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+            });
+        });
+    };
+    if (ep.bias_kind != FHIP_BIAS_NONE) epilogue(std::true_type{});
+    else epilogue(std::false_type{});
+    __syncthreads();
+    constexpr int kChunks = BN * OUT_BYTES / 16;
+    const int64_t n_bytes = ep.n * OUT_BYTES;
+    uint8_t* out = static_cast<uint8_t*>(ep.out);
+    const bool vec = (n_bytes & 15) == 0;
+    for (int q = tid; q < BM * kChunks; q += 256) {
+        const int r = q / kChunks, c = q % kChunks;
+        const int64_t row = m0 + r;
+        const int64_t colb = n0 * OUT_BYTES + c * 16;
+        if (row >= m || colb >= n_bytes) continue;
+        const uint8_t* s2 = so + r * kOutPitch + c * 16;
+        uint8_t* dst = out + row * n_bytes + colb;
+        if (vec) {
+            *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(s2);
+        } else {
+            for (int i = 0; i < 16 && colb + i < n_bytes; ++i) dst[i] = s2[i];
+        }
+    }
+}
+
+template <int BM, int BN, int OUT_BYTES>
+constexpr size_t lds_bytes() {
+    constexpr size_t ops = (size_t)kStages * Stage<BM, BN>::kBytes;
+    constexpr size_t epi = (size_t)BM * (BN * OUT_BYTES + 16);
+    return ops > epi ? ops : epi;
+}
+
+template <bool E5, int BM, int BN, int WAVES_M, int WAVES_N>
+int launch_tile(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, const fhip_weight_s* w,
+                const Fp8Epilogue& ep, const char* name) {
+    const int64_t kp = ((w->k + 127) / 128) * 128;
+    const int64_t np = ((w->n + 255) / 256) * 256;
+    const int tiles_m = (int)((m + BM - 1) / BM), tiles_n = (int)((w->n + BN - 1) / BN);
+    const int tiles = tiles_m * tiles_n;
+    const int grid = tiles;  // the kernel remaps tiles XCD-wise when the count divides by 8
+    const uint8_t* wd = static_cast<const uint8_t*>(w->data);
+    const bool pow2 = ep.out_inv != 0.0f;
+#define FHIP_GEMM_LAUNCH(OB, P)                                                                                     \
+    fp8_gemm_kernel<E5, BM, BN, WAVES_M, WAVES_N, OB, P><<<grid, 256, lds_bytes<BM, BN, OB>(), ctx->stream>>>(     \
+        a, m, k64, wd, kp, np, tiles_n, tiles, ep)
+    if (ep.out_dtype == FHIP_FP32) {
+        if (lds_bytes<BM, BN, 4>() > 160 * 1024)
+            return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "fp8 gemm: fp32 output tile too large");
+        if (pow2) FHIP_GEMM_LAUNCH(4, true); else FHIP_GEMM_LAUNCH(4, false);
+    } else if (ep.out_dtype == FHIP_BF16) {
+        if (pow2) FHIP_GEMM_LAUNCH(2, true); else FHIP_GEMM_LAUNCH(2, false);
+    } else {
+        if (pow2) FHIP_GEMM_LAUNCH(1, true); else FHIP_GEMM_LAUNCH(1, false);
+    }
+#undef FHIP_GEMM_LAUNCH
+    ctx->last_backend = name;
+    FHIP_CHECK_LAUNCH(ctx, "fp8_gemm_kernel");
+    return FHIP_OK;
+}
+
+template <bool E5>
+int launch(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, const fhip_weight_s* w, const Fp8Epilogue& ep) {
+    const int64_t n = w->n;
+    if (ep.out_dtype == FHIP_FP32) return launch_tile<E5, 128, 128, 2, 2>(ctx, a, m, k64, w, ep, "fp8_mfma_gemm_128x128");
+    // Tile choice: fill the 256 CUs with whole tiles where the shape allows it.
+    if (n % 224 == 0 && ((m + 255) / 256) * (n / 224) >= 192)
+        return launch_tile<E5, 256, 224, 4, 1>(ctx, a, m, k64, w, ep, "fp8_mfma_gemm_256x224");
+    if (((m + 255) / 256) * ((n + 255) / 256) >= 192)
+        return launch_tile<E5, 256, 256, 2, 2>(ctx, a, m, k64, w, ep, "fp8_mfma_gemm_256x256");
+    return launch_tile<E5, 128, 128, 2, 2>(ctx, a, m, k64, w, ep, "fp8_mfma_gemm_128x128");
+}
+
+}  // namespace
+
+int fhip::launch_fp8_gemm(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, const fhip_weight_s* w,
+                          const Fp8Epilogue& ep) {
+    return ep.e5 ? launch<true>(ctx, a, m, k64, w, ep) : launch<false>(ctx, a, m, k64, w, ep);
+}

@@ -12,86 +12,17 @@
 //   * fp8_gemv_kernel   -- decode rows (m <= 16): bandwidth-bound.  Weight rows stream from HBM
 //                          with 16-byte loads, activations are staged once per block in LDS as FP8
 //                          codes, products accumulate on the VALU, a cross-lane butterfly reduces.
-//   * fp8_mfma_gemm_kernel -- prefill (m > 16): v_mfma_scale_f32_16x16x128_f8f6f4 with unit
-//                          block scales, fp32 accumulation.
+//   * fp8_gemm_kernel (fp8_gemm.hip) -- prefill (m > 16): MFMA, fp32 accumulation.
 // Weights come prepared as [Np][Kp] (K contiguous, zero padded; runtime.hip).
-#include "fhip_internal.h"
+#include "fp8_common.h"
 
 #include <cmath>
 #include "codec.h"
 #include "wave.h"
 
+using namespace fhip;
+
 namespace {
-
-typedef int v8i __attribute__((ext_vector_type(8)));
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef float v2f __attribute__((ext_vector_type(2)));
-
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-// 16-byte streaming load (non-temporal: the weight is read once per call).
-__device__ __forceinline__ uint4 load_stream16(const uint8_t* p) {
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-
-// Decodes four FP8 codes packed little-endian in `w` with the hardware OCP converters.
-template <bool E5>
-__device__ __forceinline__ void decode4(uint32_t w, float* out) {
-    v2f lo, hi;
-    if constexpr (E5) {
-        lo = __builtin_amdgcn_cvt_pk_f32_bf8((int)w, false);
-        hi = __builtin_amdgcn_cvt_pk_f32_bf8((int)w, true);
-    } else {
-        lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
-        hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
-    }
-    out[0] = lo.x;
-    out[1] = lo.y;
-    out[2] = hi.x;
-    out[3] = hi.y;
-}
-
-struct Fp8Epilogue {
-    float ab_scale;      // a_scale * w_scale
-    float alpha, beta;
-    const uint8_t* bias;
-    float bias_scale;
-    int bias_kind;
-    float out_scale;
-    float out_inv;       // 1/out_scale when out_scale is a power of two, else 0 (divide)
-    int out_dtype;       // FP8 (code), BF16 or FP32 (decoded through the FP8 code)
-    void* out;
-    int64_t n;           // row stride of out
-    bool e5;
-
-    __device__ __forceinline__ void store(float acc, int64_t row, int64_t col) const {
-        float y = acc * ab_scale;
-        if (bias_kind != FHIP_BIAS_NONE) {
-            y *= alpha;
-            const uint8_t bc = bias[bias_kind == FHIP_BIAS_VECTOR ? col : row * n + col];
-            y += beta * (fhip::fp8_decode(bc, e5) * bias_scale);
-        } else {
-            y *= alpha;
-        }
-        const uint8_t code = fhip::fp8_encode(out_inv != 0.0f ? y * out_inv : y / out_scale, e5);
-        const int64_t idx = row * n + col;
-        if (out_dtype == FHIP_BF16) {
-            static_cast<uint16_t*>(out)[idx] = fhip::bf16_encode(fhip::fp8_decode(code, e5) * out_scale);
-        } else if (out_dtype == FHIP_FP32) {
-            static_cast<float*>(out)[idx] = fhip::fp8_decode(code, e5) * out_scale;
-        } else {
-            static_cast<uint8_t*>(out)[idx] = code;
-        }
-    }
-};
-
-constexpr int kGemvThreads = 256;
-constexpr int kGemvMaxLds = 64 * 1024;
-#ifndef FHIP_GEMV_R1
-#define FHIP_GEMV_R1 2
-#endif
 
 // Activation staging: the block encodes its activation rows once into LDS as FP8 codes.  Every
 // thread takes groups of 4 elements (one 4/8/16-byte load for FP8/BF16/FP32) and issues all of its
@@ -251,70 +182,28 @@ __global__ __launch_bounds__(kGemvThreads) void fp8_gemv_kernel(const void* __re
         }
 }
 
-// ---- MFMA GEMM (first version: operands straight from global/L2 into registers) -------------
-// Block: 4 waves in a 2 x 2 arrangement, wave tile (16*WM) x (16*WN), block tile (32*WM) x (32*WN).
-// A: [m][k] FP8 codes (row-major), B: prepared [Np][Kp].  k step 128 (one MFMA depth).
-// Operand fragment of lane l: row/col l%16, bytes [32*(l/16), 32*(l/16)+32) of the 128-deep
-// slice, for A and B alike, so both index the same k for every MFMA slot.
-template <bool E5, int WM, int WN>
-__global__ __launch_bounds__(256) void fp8_mfma_gemm_kernel(const uint8_t* __restrict__ a, int64_t m, int64_t k,
-                                                            const uint8_t* __restrict__ b, int64_t kp,
-                                                            Fp8Epilogue ep) {
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int64_t row_base = (int64_t)blockIdx.y * (32 * WM) + (wave >> 1) * (16 * WM);
-    const int64_t col_base = (int64_t)blockIdx.x * (32 * WN) + (wave & 1) * (16 * WN);
-    const int frag_row = lane & 15;
-    const int frag_k = (lane >> 4) * 32;
-    constexpr int fmt = E5 ? 1 : 0;
-
-    v4f acc[WM][WN];
-#pragma unroll
-    for (int i = 0; i < WM; ++i)
-#pragma unroll
-        for (int j = 0; j < WN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-
-    for (int64_t k0 = 0; k0 < k; k0 += 128) {
-        v8i af[WM], bf[WN];
-#pragma unroll
-        for (int i = 0; i < WM; ++i) {
-            const int64_t row = row_base + i * 16 + frag_row;
-            const int64_t kk = k0 + frag_k;
-            uint4 lo = make_uint4(0, 0, 0, 0), hi = make_uint4(0, 0, 0, 0);
-            if (row < m) {
-                const uint8_t* p = a + row * k + kk;
-                if (kk < k) lo = *reinterpret_cast<const uint4*>(p);
-                if (kk + 16 < k) hi = *reinterpret_cast<const uint4*>(p + 16);
+// ---- GEMM operand staging: FP8 codes [m][k64], k64 = k rounded up to 64, zero padded; BF16/FP32
+// activations are encoded with the preceding Cast node's rule Enc(x / a_scale).
+__global__ void stage_gemm_a_kernel(const void* __restrict__ a, int a_dtype, float a_scale, float a_inv, int64_t m,
+                                    int64_t k, int64_t k64, uint8_t* __restrict__ dst, bool e5) {
+    const int64_t total = m * k64;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / k64, kk = i - r * k64;
+        uint8_t code = 0;
+        if (kk < k) {
+            const int64_t e = r * k + kk;
+            if (a_dtype == FHIP_BF16) {
+                const float x = fhip::bf16_decode(static_cast<const uint16_t*>(a)[e]);
+                code = fhip::fp8_encode(a_inv != 0.0f ? x * a_inv : x / a_scale, e5);
+            } else if (a_dtype == FHIP_FP32) {
+                const float x = static_cast<const float*>(a)[e];
+                code = fhip::fp8_encode(a_inv != 0.0f ? x * a_inv : x / a_scale, e5);
+            } else {
+                code = static_cast<const uint8_t*>(a)[e];
             }
-            af[i] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
         }
-#pragma unroll
-        for (int j = 0; j < WN; ++j) {
-            const uint8_t* p = b + (col_base + j * 16 + frag_row) * kp + k0 + frag_k;
-            const uint4 lo = *reinterpret_cast<const uint4*>(p);
-            const uint4 hi = *reinterpret_cast<const uint4*>(p + 16);
-            bf[j] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-        }
-#pragma unroll
-        for (int i = 0; i < WM; ++i)
-#pragma unroll
-            for (int j = 0; j < WN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[i], bf[j], acc[i][j], fmt, fmt, 0, 127,
-                                                                             0, 127);
+        dst[i] = code;
     }
-    // C fragment of lane l: column l%16, rows 4*(l/16) .. +3.
-#pragma unroll
-    for (int i = 0; i < WM; ++i)
-#pragma unroll
-        for (int j = 0; j < WN; ++j) {
-            const int64_t col = col_base + j * 16 + (lane & 15);
-            if (col >= ep.n) continue;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t row = row_base + i * 16 + (lane >> 4) * 4 + r;
-                if (row < m) ep.store(acc[i][j][r], row, col);
-            }
-        }
 }
 
 // ---- Cast ------------------------------------------------------------------------------------
@@ -342,15 +231,6 @@ __global__ void cast_kernel(const void* __restrict__ src, int src_dtype, float s
             default: static_cast<uint8_t*>(dst)[i] = fhip::fp8_encode(v / dst_scale, true); break;
         }
     }
-}
-
-// 1/s when s is a power of two (exact), else 0.
-float pow2_inverse(float s) {
-    int e = 0;
-    const float f = std::frexp(s, &e);
-    if (f != 0.5f) return 0.0f;
-    const float inv = std::ldexp(1.0f, 1 - e);
-    return std::isfinite(inv) && inv * s == 1.0f ? inv : 0.0f;
 }
 
 bool is_fp8(int d) { return d == FHIP_FP8E4M3 || d == FHIP_FP8E5M2; }
@@ -398,19 +278,15 @@ int launch_gemv(fhip_context ctx, const void* a, int a_dtype, float a_scale, int
     return launch_gemv_t<E5, 0>(ctx, a, a_scale, m, w, ep);
 }
 
-template <bool E5>
-int launch_gemm(fhip_context ctx, const uint8_t* a, int64_t m, const fhip_weight_s* w, const Fp8Epilogue& ep) {
-    const int64_t kp = ((w->k + 127) / 128) * 128;
-    constexpr int WM = 4, WN = 4;
-    dim3 grid((unsigned)((w->n + 32 * WN - 1) / (32 * WN)), (unsigned)((m + 32 * WM - 1) / (32 * WM)));
-    fp8_mfma_gemm_kernel<E5, WM, WN><<<grid, 256, 0, ctx->stream>>>(a, m, w->k, static_cast<const uint8_t*>(w->data),
-                                                                    kp, ep);
-    ctx->last_backend = "fp8_mfma_gemm_128x128";
-    FHIP_CHECK_LAUNCH(ctx, "fp8_mfma_gemm_kernel");
-    return FHIP_OK;
-}
-
 }  // namespace
+
+float fhip::pow2_inverse(float s) {
+    int e = 0;
+    const float f = std::frexp(s, &e);
+    if (f != 0.5f) return 0.0f;
+    const float inv = std::ldexp(1.0f, 1 - e);
+    return std::isfinite(inv) && inv * s == 1.0f ? inv : 0.0f;
+}
 
 extern "C" {
 
@@ -451,18 +327,19 @@ int fhip_fp8_linear(fhip_context ctx, int a_dtype, const void* a, float a_scale,
         return e5 ? launch_gemv<true>(ctx, a, a_dtype, a_scale, m, w, ep)
                   : launch_gemv<false>(ctx, a, a_dtype, a_scale, m, w, ep);
     }
-    if (w->k % 16 != 0)
-        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "fp8_linear: MFMA path needs K % 16 == 0");
+    // MFMA path: A must be FP8 codes with K a multiple of 64 and 16-byte aligned rows.
     const uint8_t* codes = static_cast<const uint8_t*>(a);
-    if (a_dtype != w->dtype) {
+    const int64_t k64 = (w->k + 63) / 64 * 64;
+    if (a_dtype != w->dtype || k64 != w->k || (reinterpret_cast<uintptr_t>(a) & 15) != 0) {
         void* ws = nullptr;
-        int rc = fhip::acquire_workspace(ctx, (size_t)(m * w->k), &ws);
+        int rc = fhip::acquire_workspace(ctx, (size_t)(m * k64), &ws);
         if (rc != FHIP_OK) return rc;
-        rc = fhip_cast(ctx, a_dtype, a, 1.0f, m * w->k, w->dtype, ws, a_scale);
-        if (rc != FHIP_OK) return rc;
+        stage_gemm_a_kernel<<<grid_for(m * k64, 256), 256, 0, ctx->stream>>>(a, a_dtype, a_scale, pow2_inverse(a_scale),
+                                                                              m, w->k, k64, static_cast<uint8_t*>(ws), e5);
+        FHIP_CHECK_LAUNCH(ctx, "stage_gemm_a_kernel");
         codes = static_cast<const uint8_t*>(ws);
     }
-    return e5 ? launch_gemm<true>(ctx, codes, m, w, ep) : launch_gemm<false>(ctx, codes, m, w, ep);
+    return fhip::launch_fp8_gemm(ctx, codes, m, k64, w, ep);
 }
 
 }  // extern "C"
