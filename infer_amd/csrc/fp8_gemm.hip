@@ -41,14 +41,16 @@ __device__ __forceinline__ void static_for(F&& f) {
 // wave issues the same number of 16-byte loads).  Rows are unpadded; the 16-byte chunk c of row r
 // sits at position c ^ swz(r), swz(r) = (r >> 2) & 3, which keeps the 16 lanes of every
 // ds_read_b128 group on 16 distinct 4-bank groups.
-template <int BM, int BN>
+template <int BM, int BN, int NT>
 struct Stage {
-    static constexpr int BNP = (BN + 63) / 64 * 64;
+    static constexpr int kRowsPerPass = NT / 4;    // one pass of 16-byte loads covers NT/4 rows
+    static constexpr int BNP = (BN + kRowsPerPass - 1) / kRowsPerPass * kRowsPerPass;
     static constexpr int kA = BM * kBK;
     static constexpr int kBytes = (BM + BNP) * kBK;
-    static constexpr int kLoadsA = BM * 4 / 256;   // 16-byte loads per thread per stage
-    static constexpr int kLoadsB = BNP * 4 / 256;
+    static constexpr int kLoadsA = BM * 4 / NT;    // 16-byte loads per thread per stage
+    static constexpr int kLoadsB = BNP * 4 / NT;
     static constexpr int kLoads = kLoadsA + kLoadsB;
+    static_assert(kLoadsA * NT == BM * 4, "BM must be a multiple of NT/4");
 };
 
 __device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
@@ -164,10 +166,11 @@ __device__ __forceinline__ void fast_value4(const Fp8Epilogue& ep, float mul, co
 }
 
 template <bool E5, int BM, int BN, int WAVES_M, int WAVES_N, int OUT_BYTES, bool POW2>
-__global__ __launch_bounds__(256) void fp8_gemm_kernel(const uint8_t* __restrict__ a, int64_t m, int64_t k,
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const uint8_t* __restrict__ a, int64_t m, int64_t k,
                                                        const uint8_t* __restrict__ b, int64_t kp, int64_t np,
                                                        int tiles_n, int tiles_total, Fp8Epilogue ep) {
-    using S = Stage<BM, BN>;
+    constexpr int NT = 64 * WAVES_M * WAVES_N;
+    using S = Stage<BM, BN, NT>;
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int FM = WTM / 32, FN = WTN / 32;
     static_assert(FM * 32 == WTM && FN * 32 == WTN, "wave tile must be a multiple of 32");
@@ -191,7 +194,7 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(const uint8_t* __restrict
 #pragma unroll
     for (int i = 0; i < S::kLoads; ++i) {
         const bool is_a = i < S::kLoadsA;
-        const int q = (is_a ? i : i - S::kLoadsA) * 256 + tid;
+        const int q = (is_a ? i : i - S::kLoadsA) * NT + tid;
         const int r = q >> 2;
         const int c = (q & 3) ^ swz(r);
         if (is_a) {
@@ -208,7 +211,7 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(const uint8_t* __restrict
         for (int i = 0; i < S::kLoads; ++i) {
             const bool is_a = i < S::kLoadsA;
             const int slot = is_a ? i : i - S::kLoadsA;
-            uint8_t* dst = st + (is_a ? 0 : S::kA) + (slot * 256 + wave * 64) * 16;
+            uint8_t* dst = st + (is_a ? 0 : S::kA) + (slot * NT + wave * 64) * 16;
             load_to_lds(src[i] + (int64_t)kt * kBK, dst);
         }
     };
@@ -236,9 +239,7 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(const uint8_t* __restrict
         // Plain s_barrier: the explicit vmcnt wait above already covers this wave's stage loads, and a
         // __syncthreads() fence would also wait for the loads of the stages still in flight.
         __builtin_amdgcn_s_barrier();
-#ifndef FHIP_GEMM_PROBE_NOLOAD
         if (kt + kStages - 1 < nk) issue(kt + kStages - 1);
-#endif
         const uint8_t* sa = smem + (kt % kStages) * S::kBytes;
         const uint8_t* sb = sa + S::kA;
         u32x4_t fa[FM][2], fb[FN][2];
@@ -259,38 +260,19 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(const uint8_t* __restrict
         // Wait for the fragment reads; every fragment register is an operand, so no MFMA that uses one
         // can be scheduled above the wait.
         lds_fence<FM, FN>(fa, fb);
-        v8i af[FM], bf[FN];
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-            af[i] = v8i{(int)fa[i][0].x, (int)fa[i][0].y, (int)fa[i][0].z, (int)fa[i][0].w,
-                        (int)fa[i][1].x, (int)fa[i][1].y, (int)fa[i][1].z, (int)fa[i][1].w};
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-            bf[j] = v8i{(int)fb[j][0].x, (int)fb[j][0].y, (int)fb[j][0].z, (int)fb[j][0].w,
-                        (int)fb[j][1].x, (int)fb[j][1].y, (int)fb[j][1].z, (int)fb[j][1].w};
-#ifndef FHIP_GEMM_PROBE_NOMFMA
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
-            for (int j = 0; j < FN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af[i], acc[i][j], fmt, fmt, 0, 127,
-                                                                            0, 127);
-#endif
+            for (int j = 0; j < FN; ++j) {
+                const v8i av = v8i{(int)fa[i][0].x, (int)fa[i][0].y, (int)fa[i][0].z, (int)fa[i][0].w,
+                                   (int)fa[i][1].x, (int)fa[i][1].y, (int)fa[i][1].z, (int)fa[i][1].w};
+                const v8i bv = v8i{(int)fb[j][0].x, (int)fb[j][0].y, (int)fb[j][0].z, (int)fb[j][0].w,
+                                   (int)fb[j][1].x, (int)fb[j][1].y, (int)fb[j][1].z, (int)fb[j][1].w};
+                // weight fragment as the row operand: each 32x32 block is computed transposed
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[i][j], fmt, fmt, 0, 127, 0, 127);
+            }
     }
     __syncthreads();
-#ifdef FHIP_GEMM_PROBE_NOEPI
-    {
-        float t = 0.0f;
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) t += acc[i][j][e];
-        if (t == 12345.0f) static_cast<uint8_t*>(ep.out)[tid] = 1;
-        return;
-    }
-#endif
 
     // ---- epilogue.  The MFMA computed each 32x32 block transposed (weight fragment as the row operand),
     // so lane l holds output row m = l%32 of the block and, for e = 4g..4g+3, the four consecutive
@@ -326,7 +308,7 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(const uint8_t* __restrict
     const int64_t n_bytes = ep.n * OUT_BYTES;
     uint8_t* out = static_cast<uint8_t*>(ep.out);
     const bool vec = (n_bytes & 15) == 0;
-    for (int q = tid; q < BM * kChunks; q += 256) {
+    for (int q = tid; q < BM * kChunks; q += NT) {
         const int r = q / kChunks, c = q % kChunks;
         const int64_t row = m0 + r;
         const int64_t colb = n0 * OUT_BYTES + c * 16;
@@ -341,9 +323,9 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(const uint8_t* __restrict
     }
 }
 
-template <int BM, int BN, int OUT_BYTES>
+template <int BM, int BN, int NT, int OUT_BYTES>
 constexpr size_t lds_bytes() {
-    constexpr size_t ops = (size_t)kStages * Stage<BM, BN>::kBytes;
+    constexpr size_t ops = (size_t)kStages * Stage<BM, BN, NT>::kBytes;
     constexpr size_t epi = (size_t)BM * (BN * OUT_BYTES + 16);
     return ops > epi ? ops : epi;
 }
@@ -359,10 +341,11 @@ int launch_tile(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, cons
     const uint8_t* wd = static_cast<const uint8_t*>(w->data);
     const bool pow2 = ep.out_inv != 0.0f;
 #define FHIP_GEMM_LAUNCH(OB, P)                                                                                     \
-    fp8_gemm_kernel<E5, BM, BN, WAVES_M, WAVES_N, OB, P><<<grid, 256, lds_bytes<BM, BN, OB>(), ctx->stream>>>(     \
+    fp8_gemm_kernel<E5, BM, BN, WAVES_M, WAVES_N, OB, P><<<grid, 64 * WAVES_M * WAVES_N,                             \
+                                                          lds_bytes<BM, BN, 64 * WAVES_M * WAVES_N, OB>(), ctx->stream>>>( \
         a, m, k64, wd, kp, np, tiles_n, tiles, ep)
     if (ep.out_dtype == FHIP_FP32) {
-        if (lds_bytes<BM, BN, 4>() > 160 * 1024)
+        if (lds_bytes<BM, BN, 64 * WAVES_M * WAVES_N, 4>() > 160 * 1024)
             return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "fp8 gemm: fp32 output tile too large");
         if (pow2) FHIP_GEMM_LAUNCH(4, true); else FHIP_GEMM_LAUNCH(4, false);
     } else if (ep.out_dtype == FHIP_BF16) {
@@ -379,13 +362,11 @@ int launch_tile(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, cons
 template <bool E5>
 int launch(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, const fhip_weight_s* w, const Fp8Epilogue& ep) {
     const int64_t n = w->n;
-    if (ep.out_dtype == FHIP_FP32) return launch_tile<E5, 128, 128, 2, 2>(ctx, a, m, k64, w, ep, "fp8_mfma_gemm_128x128");
+    if (ep.out_dtype == FHIP_FP32) return launch_tile<E5, 128, 128, 2, 4>(ctx, a, m, k64, w, ep, "fp8_mfma_gemm_128x128_w8");
     // Tile choice: fill the 256 CUs with whole tiles where the shape allows it.
-    if (n % 224 == 0 && ((m + 255) / 256) * (n / 224) >= 192)
-        return launch_tile<E5, 256, 224, 4, 1>(ctx, a, m, k64, w, ep, "fp8_mfma_gemm_256x224");
     if (((m + 255) / 256) * ((n + 255) / 256) >= 192)
-        return launch_tile<E5, 256, 256, 2, 2>(ctx, a, m, k64, w, ep, "fp8_mfma_gemm_256x256");
-    return launch_tile<E5, 128, 128, 2, 2>(ctx, a, m, k64, w, ep, "fp8_mfma_gemm_128x128");
+        return launch_tile<E5, 256, 256, 4, 2>(ctx, a, m, k64, w, ep, "fp8_mfma_gemm_256x256_w8");
+    return launch_tile<E5, 128, 128, 2, 4>(ctx, a, m, k64, w, ep, "fp8_mfma_gemm_128x128_w8");
 }
 
 }  // namespace
