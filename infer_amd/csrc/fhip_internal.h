@@ -58,6 +58,7 @@ struct fhip_weight_s {
     float* scales = nullptr;     // [n] device (INT8)
     int32_t* zps = nullptr;      // [n] device (INT8)
     int32_t* wsum = nullptr;     // [n] device: sum_k (w - zp_w) per output channel (INT8)
+    void* tap_major = nullptr;   // conv (group 1): [OC][KH*KW][IC] copy for the LDS-window kernel
     bool per_channel = false;
     float scale0 = 1.0f;
     int32_t zp0 = 0;

@@ -228,6 +228,160 @@ __global__ __launch_bounds__(256) void i8_conv_kernel(const int8_t* __restrict__
         }
 }
 
+// ---- INT8 Conv2D, LDS-window implicit GEMM (group 1, IC a multiple of 64) -----------------------
+// A block owns kConvTox consecutive output x positions of one output row (b, oy) and 64*WNF output
+// channels per wave.  For each 64-channel chunk it stages the input window the row segment needs --
+// KH rows x WX columns x 64 channels, channel-last, out-of-image taps filled with zp_in -- into LDS.
+// Every A fragment (16 pixels x 16 channels of one tap) is then a single ds_read_b128; the weight is
+// the tap-major copy [OC][KH*KW][IC], so a B fragment is one 16-byte load.  K runs over
+// (chunk, ky, kx, 64 channels) with v_mfma_i32_16x16x64_i8; integer accumulation is exact, so the
+// order differs from the reference's (ci, ky, kx) order without changing any sum.
+constexpr int kConvTox = 32;
+constexpr int kConvPitch = 80;  // 64 channels + 16 bytes: stride-2 fragment reads spread over banks
+
+template <int WNF, int TAPS>
+__global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __restrict__ in, ConvGeom g,
+                                                             const int8_t* __restrict__ wt,
+                                                             const int32_t* __restrict__ bias, I8Epilogue ep,
+                                                             int64_t oc_total) {
+    extern __shared__ __align__(16) uint8_t win[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int64_t ox0 = (int64_t)blockIdx.x * kConvTox;
+    const int64_t b = blockIdx.y / g.oh, oy = blockIdx.y % g.oh;
+    const int64_t oc_base = (int64_t)blockIdx.z * (4 * WNF * 16) + wave * (WNF * 16);
+    const int wx = (kConvTox - 1) * g.sw + (int)((g.kw - 1) * g.dw) + 1;
+    const int64_t taps = g.kh * g.kw;
+    const int kq = (lane >> 4) * 16;  // channel quarter of this lane's fragment
+    v4i acc[2][WNF];
+#pragma unroll
+    for (int f = 0; f < 2; ++f)
+#pragma unroll
+        for (int j = 0; j < WNF; ++j) acc[f][j] = v4i{0, 0, 0, 0};
+
+    auto load_b = [&](int64_t tap, int64_t c0, v4i (&bf)[WNF]) {
+#pragma unroll
+        for (int j = 0; j < WNF; ++j) {
+            int64_t oc = oc_base + j * 16 + (lane & 15);
+            oc = oc < oc_total ? oc : oc_total - 1;  // clamped rows are computed, never stored
+            const uint4 v = *reinterpret_cast<const uint4*>(wt + (oc * taps + tap) * g.c + c0 + kq);
+            bf[j] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+        }
+    };
+    for (int64_t c0 = 0; c0 < g.c; c0 += 64) {
+        // weight fragments of every tap are requested first, so they arrive while the window is staged
+        v4i bpre[TAPS > 0 ? TAPS : 1][WNF];
+        if constexpr (TAPS > 0) {
+#pragma unroll
+            for (int t = 0; t < TAPS; ++t) load_b(t, c0, bpre[t]);
+        }
+        __syncthreads();
+        // stage the window
+        if (g.layout == FHIP_NCHW) {
+            // every load of the pass is issued before any LDS store (one memory round trip per pass)
+            constexpr int kBatch = 64;
+            const int total = (int)g.kh * 64 * wx;
+            for (int base = tid; base < total; base += 256 * kBatch) {
+                uint8_t v[kBatch];
+                int slot[kBatch];
+#pragma unroll
+                for (int u = 0; u < kBatch; ++u) {
+                    const int idx = base + u * 256;
+                    slot[u] = -1;
+                    v[u] = (uint8_t)g.zp_in;
+                    if (idx < total) {
+                        const int x = idx % wx, t = idx / wx;
+                        const int ci = t % 64, ky = t / 64;
+                        const int64_t iy = oy * g.sh - g.ph + ky * g.dh;
+                        const int64_t ix = ox0 * g.sw - g.pw + x;
+                        slot[u] = (ky * wx + x) * kConvPitch + ci;
+                        if (iy >= 0 && iy < g.h && ix >= 0 && ix < g.w)
+                            v[u] = (uint8_t)in[((b * g.c + c0 + ci) * g.h + iy) * g.w + ix];
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < kBatch; ++u)
+                    if (slot[u] >= 0) win[slot[u]] = v[u];
+            }
+        } else {
+            const int total = (int)g.kh * wx * 4;  // 16-byte quarters
+            for (int idx = tid; idx < total; idx += 256) {
+                const int q = idx & 3, t = idx >> 2;
+                const int x = t % wx, ky = t / wx;
+                const int64_t iy = oy * g.sh - g.ph + ky * g.dh;
+                const int64_t ix = ox0 * g.sw - g.pw + x;
+                uint4 v;
+                const uint32_t z = (uint32_t)(uint8_t)g.zp_in * 0x01010101u;
+                if (iy >= 0 && iy < g.h && ix >= 0 && ix < g.w)
+                    v = *reinterpret_cast<const uint4*>(in + ((b * g.h + iy) * g.w + ix) * g.c + c0 + q * 16);
+                else
+                    v = make_uint4(z, z, z, z);
+                *reinterpret_cast<uint4*>(win + (ky * wx + x) * kConvPitch + q * 16) = v;
+            }
+        }
+        __syncthreads();
+        auto tap_step = [&](int64_t ky, int64_t kx, const v4i (&bf)[WNF]) {
+            v4i af[2];
+#pragma unroll
+            for (int f = 0; f < 2; ++f) {
+                const int p = f * 16 + (lane & 15);
+                const int x = p * g.sw + (int)(kx * g.dw);
+                const uint4 v = *reinterpret_cast<const uint4*>(win + (ky * wx + x) * kConvPitch + kq);
+                af[f] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+            }
+#pragma unroll
+            for (int f = 0; f < 2; ++f)
+#pragma unroll
+                for (int j = 0; j < WNF; ++j)
+                    acc[f][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[f], bf[j], acc[f][j], 0, 0, 0);
+        };
+        if constexpr (TAPS > 0) {
+#pragma unroll
+            for (int t = 0; t < TAPS; ++t) tap_step(t / g.kw, t % g.kw, bpre[t]);
+        } else {
+            for (int64_t ky = 0; ky < g.kh; ++ky)
+                for (int64_t kx = 0; kx < g.kw; ++kx) {
+                    v4i bf[WNF];
+                    load_b(ky * g.kw + kx, c0, bf);
+                    tap_step(ky, kx, bf);
+                }
+        }
+    }
+    // C fragment of lane l: channel l%16, pixels 4*(l/16) .. +3 (consecutive output x).
+#pragma unroll
+    for (int f = 0; f < 2; ++f)
+#pragma unroll
+        for (int j = 0; j < WNF; ++j) {
+            const int64_t oc = oc_base + j * 16 + (lane & 15);
+            if (oc >= oc_total) continue;
+            const double scale = (double)ep.s_a * (double)ep.w_scales[oc];
+            const int32_t shift = (bias ? bias[oc] : 0) - (int32_t)g.zp_in * ep.wsum[oc];
+            int8_t q[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const double real = (double)(acc[f][j][r] + shift) * scale;
+                q[r] = clamp_round_i8(real / ep.inv_out_den + ep.zp_out);
+            }
+            const int64_t ox = ox0 + f * 16 + (lane >> 4) * 4;
+            if (g.layout == FHIP_NCHW) {
+                int8_t* dst = ep.out + ((b * oc_total + oc) * g.oh + oy) * g.ow + ox;
+                if (ox + 3 < g.ow && ((reinterpret_cast<uintptr_t>(dst) & 3) == 0)) {
+                    *reinterpret_cast<uint32_t*>(dst) = (uint32_t)(uint8_t)q[0] | ((uint32_t)(uint8_t)q[1] << 8) |
+                                                        ((uint32_t)(uint8_t)q[2] << 16) | ((uint32_t)(uint8_t)q[3] << 24);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (ox + r < g.ow) dst[r] = q[r];
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (ox + r < g.ow) ep.out[((b * g.oh + oy) * g.ow + ox + r) * oc_total + oc] = q[r];
+            }
+        }
+}
+
 // ---- QuantizeLinear / DequantizeLinear ---------------------------------------------------------
 constexpr int kInlineChannels = 128;
 struct QParams {
@@ -378,6 +532,26 @@ int fhip_i8_conv2d(fhip_context ctx, const int8_t* in, int64_t n, int64_t c, int
                stride_h, stride_w, pad_h, pad_w, dil_h, dil_w, layout, (int8_t)zp_in};
     I8Epilogue ep{FHIP_I8_FC, wt->scales, wt->wsum, nullptr, FHIP_BIAS_NONE, zp_in, s_in, 1.0, 1.0, (double)s_out,
                   (double)zp_out, out, 0};
+    if (wt->tap_major && c % 64 == 0 && wt->group == 1 &&
+        (layout == FHIP_NCHW || (reinterpret_cast<uintptr_t>(in) & 15) == 0)) {
+        const int wx = (kConvTox - 1) * stride_w + (int)((wt->kw - 1) * dil_w) + 1;
+        const size_t lds = (size_t)wt->kh * wx * kConvPitch;
+        if (lds <= 64 * 1024) {
+            const int64_t oc = wt->n;
+            const int wnf = oc >= 128 ? 2 : 1;
+            dim3 grid((unsigned)((ow + kConvTox - 1) / kConvTox), (unsigned)(n * oh),
+                      (unsigned)((oc + 4 * wnf * 16 - 1) / (4 * wnf * 16)));
+            const int8_t* tm = static_cast<const int8_t*>(wt->tap_major);
+            const bool t9 = wt->kh * wt->kw == 9;
+            if (wnf == 2 && t9) i8_conv_window_kernel<2, 9><<<grid, 256, lds, ctx->stream>>>(in, g, tm, bias, ep, oc);
+            else if (wnf == 2) i8_conv_window_kernel<2, 0><<<grid, 256, lds, ctx->stream>>>(in, g, tm, bias, ep, oc);
+            else if (t9) i8_conv_window_kernel<1, 9><<<grid, 256, lds, ctx->stream>>>(in, g, tm, bias, ep, oc);
+            else i8_conv_window_kernel<1, 0><<<grid, 256, lds, ctx->stream>>>(in, g, tm, bias, ep, oc);
+            ctx->last_backend = "i8_mfma_conv_window";
+            FHIP_CHECK_LAUNCH(ctx, "i8_conv_window_kernel");
+            return FHIP_OK;
+        }
+    }
     constexpr int WM = 2, WN = 2;
     const int64_t np = n * oh * ow;
     dim3 grid((unsigned)((g.ocg + 32 * WN - 1) / (32 * WN)), (unsigned)((np + 32 * WM - 1) / (32 * WM)),

@@ -117,8 +117,19 @@ __global__ void weight_channel_stats_kernel(const int8_t* __restrict__ w, int64_
     }
 }
 
+// Conv weight [OC][IC][KH][KW] -> tap-major [OC][KH*KW][IC] (channels contiguous per tap).
+__global__ void conv_tap_major_kernel(const int8_t* __restrict__ src, int64_t ic, int64_t taps,
+                                      int8_t* __restrict__ dst) {
+    const int64_t oc = blockIdx.x;
+    for (int64_t i = threadIdx.x; i < ic * taps; i += blockDim.x) {
+        const int64_t t = i / ic, c = i - t * ic;
+        dst[(oc * taps + t) * ic + c] = src[(oc * ic + c) * taps + t];
+    }
+}
+
 void free_weight(fhip_weight w) {
     if (!w) return;
+    if (w->tap_major) (void)hipFree(w->tap_major);
     if (w->data) (void)hipFree(w->data);
     if (w->scales) (void)hipFree(w->scales);  // one allocation holds scales, zps, wsum and max|w|
     delete w;
@@ -364,6 +375,17 @@ int fhip_conv_weight_prepare(fhip_context ctx, const int8_t* src, int64_t oc, in
     w->kw = kw;
     w->group = group;
     int rc = prepare_common(ctx, w, src, k, oc, FHIP_LAYOUT_NK, scales, n_scale, zero_points, n_zp);
+    if (rc == FHIP_OK && group == 1 && icg % 64 == 0) {
+        const size_t bytes = (size_t)(oc * k);
+        if (ctx->weight_bytes + w->bytes + bytes <= ctx->weight_cache_limit &&
+            (rc = check_hip(ctx, hipMalloc(&w->tap_major, bytes), "hipMalloc(conv tap-major)")) == FHIP_OK) {
+            conv_tap_major_kernel<<<(unsigned)oc, 256, 0, ctx->stream>>>(src, icg, kh * kw,
+                                                                          static_cast<int8_t*>(w->tap_major));
+            rc = check_hip(ctx, hipGetLastError(), "conv_tap_major_kernel");
+            if (rc == FHIP_OK) rc = check_hip(ctx, hipStreamSynchronize(ctx->stream), "sync conv prepare");
+            w->bytes += bytes;
+        }
+    }
     if (rc != FHIP_OK) {
         free_weight(w);
         return rc;
