@@ -62,54 +62,84 @@ struct I8Epilogue {
 };
 
 // ---- INT8 GEMM: A [m][k] int8 row-major, B prepared [Np][Kp] ---------------------------------
-// Block: 4 waves (2 x 2), wave tile (16*WM) x (16*WN).  MFMA depth 64: lane l supplies row/col
-// l%16 and bytes [16*(l/16), 16*(l/16)+16) of the slice for both operands.
-template <int WM, int WN>
+// Block tile (16*FM) x (16*FN).  The four waves split K: wave w takes the 64-deep steps w, w+4, ...,
+// issues the loads of kUnroll steps before their MFMAs (one memory round trip per kUnroll*4 steps),
+// and the four partial tiles are summed through LDS; integer sums are exact in any order.
+// MFMA depth 64: lane l supplies row/col l%16 and bytes [16*(l/16), 16*(l/16)+16) of the step.
+constexpr int kI8Unroll = 4;
+
+template <int FM, int FN>
 __global__ __launch_bounds__(256) void i8_gemm_kernel(const int8_t* __restrict__ a, int64_t m, int64_t k,
                                                       const int8_t* __restrict__ b, int64_t kp, int64_t n,
                                                       I8Epilogue ep) {
+    constexpr int TM = 16 * FM, TN = 16 * FN;
+    __shared__ int32_t red[4][TM][TN + 1];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int64_t row_base = (int64_t)blockIdx.y * (32 * WM) + (wave >> 1) * (16 * WM);
-    const int64_t col_base = (int64_t)blockIdx.x * (32 * WN) + (wave & 1) * (16 * WN);
+    const int64_t row_base = (int64_t)blockIdx.y * TM;
+    const int64_t col_base = (int64_t)blockIdx.x * TN;
     const int fr = lane & 15;
     const int fk = (lane >> 4) * 16;
-    v4i acc[WM][WN];
+    const int8_t* arow[FM];
+    bool arow_ok[FM];
 #pragma unroll
-    for (int i = 0; i < WM; ++i)
-#pragma unroll
-        for (int j = 0; j < WN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
-    for (int64_t k0 = 0; k0 < k; k0 += 64) {
-        v4i af[WM], bf[WN];
-#pragma unroll
-        for (int i = 0; i < WM; ++i) {
-            const int64_t row = row_base + i * 16 + fr;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (row < m && k0 + fk < k) v = *reinterpret_cast<const uint4*>(a + row * k + k0 + fk);
-            af[i] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
-        }
-#pragma unroll
-        for (int j = 0; j < WN; ++j) {
-            const uint4 v = *reinterpret_cast<const uint4*>(b + (col_base + j * 16 + fr) * kp + k0 + fk);
-            bf[j] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
-        }
-#pragma unroll
-        for (int i = 0; i < WM; ++i)
-#pragma unroll
-            for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+    for (int i = 0; i < FM; ++i) {
+        const int64_t row = row_base + i * 16 + fr;
+        arow_ok[i] = row < m;
+        arow[i] = a + (arow_ok[i] ? row : 0) * k + fk;
     }
+    const int8_t* bcol[FN];
 #pragma unroll
-    for (int i = 0; i < WM; ++i)
+    for (int j = 0; j < FN; ++j) bcol[j] = b + (col_base + j * 16 + fr) * kp + fk;  // rows padded to 256
+    v4i acc[FM][FN];
 #pragma unroll
-        for (int j = 0; j < WN; ++j) {
-            const int64_t col = col_base + j * 16 + fr;
-            if (col >= n) continue;
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t row = row_base + i * 16 + (lane >> 4) * 4 + r;
-                if (row < m) ep.store(acc[i][j][r], row, col);
+        for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+    const int64_t steps = (k + 63) / 64;
+    for (int64_t s0 = wave; s0 < steps; s0 += 4 * kI8Unroll) {
+        v4i af[kI8Unroll][FM], bf[kI8Unroll][FN];
+#pragma unroll
+        for (int u = 0; u < kI8Unroll; ++u) {
+            const int64_t s = s0 + 4 * u;
+            const int64_t k0 = s * 64;
+            const bool live = s < steps;
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                uint4 v = make_uint4(0, 0, 0, 0);
+                if (live && arow_ok[i] && k0 + fk < k) v = *reinterpret_cast<const uint4*>(arow[i] + k0);
+                af[u][i] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+            }
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                uint4 v = make_uint4(0, 0, 0, 0);
+                if (live) v = *reinterpret_cast<const uint4*>(bcol[j] + k0);  // zero-padded past k
+                bf[u][j] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
             }
         }
+#pragma unroll
+        for (int u = 0; u < kI8Unroll; ++u)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[u][i], bf[u][j], acc[i][j], 0, 0, 0);
+    }
+    // C fragment of lane l: column l%16, rows 4*(l/16) .. +3.
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[wave][i * 16 + (lane >> 4) * 4 + r][j * 16 + fr] = acc[i][j][r];
+    __syncthreads();
+    for (int e = threadIdx.x; e < TM * TN; e += 256) {
+        const int rr = e / TN, cc = e % TN;
+        const int64_t row = row_base + rr, col = col_base + cc;
+        if (row >= m || col >= n) continue;
+        const int32_t raw = red[0][rr][cc] + red[1][rr][cc] + red[2][rr][cc] + red[3][rr][cc];
+        ep.store(raw, row, col);
+    }
 }
 
 // ---- INT8 Conv2D implicit GEMM ------------------------------------------------------------------
@@ -279,30 +309,50 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
         __syncthreads();
         // stage the window
         if (g.layout == FHIP_NCHW) {
-            // every load of the pass is issued before any LDS store (one memory round trip per pass)
-            constexpr int kBatch = 64;
-            const int total = (int)g.kh * 64 * wx;
-            for (int base = tid; base < total; base += 256 * kBatch) {
-                uint8_t v[kBatch];
-                int slot[kBatch];
+            // thread (ky, ci) copies one input row segment: wx bytes, transposed to channel-last in LDS.
+            // Index math is per row, not per byte; the column loop is pointer increments only.
+            const int ix0 = (int)(ox0 * g.sw - g.pw);
+            const bool interior = ix0 >= 0 && ix0 + wx <= (int)g.w;  // block-uniform
+            const uint8_t zp = (uint8_t)g.zp_in;
+            for (int r = tid; r < (int)g.kh * 64; r += 256) {
+                const int ci = r & 63, ky = r >> 6;
+                const int iy = (int)(oy * g.sh - g.ph) + ky * (int)g.dh;
+                uint8_t* dst = win + ky * wx * kConvPitch + ci;
+                if (iy < 0 || iy >= (int)g.h) {
+                    for (int x = 0; x < wx; ++x) dst[x * kConvPitch] = zp;
+                    continue;
+                }
+                const uint8_t* row = reinterpret_cast<const uint8_t*>(in) + ((b * g.c + c0 + ci) * g.h + iy) * g.w;
+                if (interior) {
+                    const uint8_t* src = row + ix0;
+                    int x = 0;
+                    for (; x + 8 <= wx; x += 8) {
+                        uint8_t v[8];
 #pragma unroll
-                for (int u = 0; u < kBatch; ++u) {
-                    const int idx = base + u * 256;
-                    slot[u] = -1;
-                    v[u] = (uint8_t)g.zp_in;
-                    if (idx < total) {
-                        const int x = idx % wx, t = idx / wx;
-                        const int ci = t % 64, ky = t / 64;
-                        const int64_t iy = oy * g.sh - g.ph + ky * g.dh;
-                        const int64_t ix = ox0 * g.sw - g.pw + x;
-                        slot[u] = (ky * wx + x) * kConvPitch + ci;
-                        if (iy >= 0 && iy < g.h && ix >= 0 && ix < g.w)
-                            v[u] = (uint8_t)in[((b * g.c + c0 + ci) * g.h + iy) * g.w + ix];
+                        for (int u = 0; u < 8; ++u) v[u] = src[x + u];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) dst[(x + u) * kConvPitch] = v[u];
+                    }
+                    for (; x < wx; ++x) dst[x * kConvPitch] = src[x];
+                } else {
+                    const int wlast = (int)g.w - 1;
+                    int x = 0;
+                    for (; x + 8 <= wx; x += 8) {
+                        uint8_t v[8];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) {
+                            const int ix = ix0 + x + u;
+                            const uint8_t t = row[ix < 0 ? 0 : (ix > wlast ? wlast : ix)];
+                            v[u] = (ix >= 0 && ix <= wlast) ? t : zp;
+                        }
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) dst[(x + u) * kConvPitch] = v[u];
+                    }
+                    for (; x < wx; ++x) {
+                        const int ix = ix0 + x;
+                        dst[x * kConvPitch] = (ix >= 0 && ix <= wlast) ? row[ix] : zp;
                     }
                 }
-#pragma unroll
-                for (int u = 0; u < kBatch; ++u)
-                    if (slot[u] >= 0) win[slot[u]] = v[u];
             }
         } else {
             const int total = (int)g.kh * wx * 4;  // 16-byte quarters
@@ -499,10 +549,18 @@ int fhip_i8_linear(fhip_context ctx, int kind, const int8_t* a, float s_a, int32
     I8Epilogue ep{kind, w->scales, w->wsum, bias, bias_kind, zp_a, s_a, (double)alpha, (double)beta, (double)s_out,
                   (double)zp_out, out, w->n};
     const int64_t kp = ((w->k + 127) / 128) * 128;
-    constexpr int WM = 1, WN = 2;
-    dim3 grid((unsigned)((w->n + 32 * WN - 1) / (32 * WN)), (unsigned)((m + 32 * WM - 1) / (32 * WM)));
-    i8_gemm_kernel<WM, WN><<<grid, 256, 0, ctx->stream>>>(a, m, w->k, static_cast<const int8_t*>(w->data), kp, w->n, ep);
-    ctx->last_backend = "i8_mfma_gemm_32x64";
+    // largest tile that still puts about two blocks on every CU
+    const int64_t blocks32 = ((w->n + 31) / 32) * ((m + 31) / 32);
+    const int8_t* bw = static_cast<const int8_t*>(w->data);
+    if (blocks32 >= 512) {
+        dim3 grid((unsigned)((w->n + 31) / 32), (unsigned)((m + 31) / 32));
+        i8_gemm_kernel<2, 2><<<grid, 256, 0, ctx->stream>>>(a, m, w->k, bw, kp, w->n, ep);
+        ctx->last_backend = "i8_mfma_gemm_32x32_ksplit4";
+    } else {
+        dim3 grid((unsigned)((w->n + 31) / 32), (unsigned)((m + 15) / 16));
+        i8_gemm_kernel<1, 2><<<grid, 256, 0, ctx->stream>>>(a, m, w->k, bw, kp, w->n, ep);
+        ctx->last_backend = "i8_mfma_gemm_16x32_ksplit4";
+    }
     FHIP_CHECK_LAUNCH(ctx, "i8_gemm_kernel");
     return FHIP_OK;
 }

@@ -120,6 +120,28 @@ def test_i8_gemm_zero_points_alpha_beta_ragged(ctx):
         wt.release()
 
 
+def test_i8_gemm_large_tile_path_long_k(ctx):
+    """Enough 32x32 tiles for the larger GEMM tile, and K = 1040: 17 steps of 64 with a 16-deep tail, so
+    the waves' K split runs a second unrolled round and a partial final step."""
+    r = rng(22)
+    m, k, n = 520, 1040, 1000
+    xq = r.integers(-128, 128, (m, k)).astype(np.int8)
+    w = r.integers(-127, 128, (n, k)).astype(np.int8)
+    s_w = r.uniform(1e-3, 1e-2, n).astype(np.float32)
+    bias = r.integers(-20000, 20000, n).astype(np.int32)
+    s_x, s_y, zp_a, zp_y = 0.01, 0.5, 3, -2
+    rc, ref, _ = po.i8_linear(po.I8_GEMM, xq, s_x, zp_a, w, True, s_w, None, bias, po.BIAS_VECTOR, 1.0, 1.0, s_y,
+                              zp_y)
+    assert rc == 0
+    wt = ctx.prepare_weight(dev(w), po.INT8, k, n, 1, scales=s_w, version=10)
+    out = torch.empty((m, n), dtype=torch.int8, device="cuda")
+    ctx.i8_linear(po.I8_GEMM, dev(xq), s_x, zp_a, m, wt, out, s_y, zp_y, bias=dev(bias), bias_kind=po.BIAS_VECTOR,
+                  bias_abs_max=20000)
+    assert ctx.last_backend() == "i8_mfma_gemm_32x32_ksplit4"
+    assert np.array_equal(out.cpu().numpy(), ref)
+    wt.release()
+
+
 def c4_inputs(seed=SEEDS[4], pow2=True):
     r = rng(seed)
     x = r.integers(-128, 128, (1, 64, 160, 160)).astype(np.int8)
