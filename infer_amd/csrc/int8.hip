@@ -268,6 +268,7 @@ __global__ __launch_bounds__(256) void i8_conv_kernel(const int8_t* __restrict__
 // order differs from the reference's (ci, ky, kx) order without changing any sum.
 constexpr int kConvTox = 32;
 constexpr int kConvPitch = 80;  // 64 channels + 16 bytes: stride-2 fragment reads spread over banks
+constexpr int kWinDwords = 18;  // NCHW rows staged by aligned dword loads when the window is <= 72 bytes
 
 template <int WNF, int TAPS>
 __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __restrict__ in, ConvGeom g,
@@ -313,6 +314,8 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
             // Index math is per row, not per byte; the column loop is pointer increments only.
             const int ix0 = (int)(ox0 * g.sw - g.pw);
             const bool interior = ix0 >= 0 && ix0 + wx <= (int)g.w;  // block-uniform
+            const bool dword_rows = (g.w & 3) == 0 && (reinterpret_cast<uintptr_t>(in) & 3) == 0 &&
+                                    wx <= 4 * kWinDwords;
             const uint8_t zp = (uint8_t)g.zp_in;
             for (int r = tid; r < (int)g.kh * 64; r += 256) {
                 const int ci = r & 63, ky = r >> 6;
@@ -323,7 +326,28 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
                     continue;
                 }
                 const uint8_t* row = reinterpret_cast<const uint8_t*>(in) + ((b * g.c + c0 + ci) * g.h + iy) * g.w;
-                if (interior) {
+                if (dword_rows) {
+                    // rows are 4-byte aligned: the whole segment arrives as kWinDwords aligned dword loads in
+                    // flight together; a dword is either inside the row or entirely padding.
+                    const int a0 = ix0 & ~3;  // floor to a multiple of 4 (two's complement)
+                    const int sh = ix0 - a0;
+                    const uint32_t z4 = (uint32_t)zp * 0x01010101u;
+                    uint32_t d[kWinDwords + 1];
+#pragma unroll
+                    for (int i = 0; i <= kWinDwords; ++i) {
+                        const int off = a0 + 4 * i;
+                        d[i] = z4;
+                        if (4 * i < sh + wx && off >= 0 && off < (int)g.w)
+                            d[i] = *reinterpret_cast<const uint32_t*>(row + off);
+                    }
+#pragma unroll
+                    for (int i = 0; i < kWinDwords; ++i) {
+                        const uint32_t e = __builtin_amdgcn_alignbyte(d[i + 1], d[i], (uint32_t)sh);
+#pragma unroll
+                        for (int u = 0; u < 4; ++u)
+                            if (4 * i + u < wx) dst[(4 * i + u) * kConvPitch] = (uint8_t)(e >> (8 * u));
+                    }
+                } else if (interior) {
                     const uint8_t* src = row + ix0;
                     int x = 0;
                     for (; x + 8 <= wx; x += 8) {

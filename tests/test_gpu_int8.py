@@ -193,21 +193,24 @@ def test_i8_conv_groups_dilation_zero_point(ctx, layout):
 
 
 @pytest.mark.parametrize("layout", [0, 1])
-def test_i8_conv_window_path_general_geometry(ctx, layout):
+@pytest.mark.parametrize("wd,pad", [(23, (1, 0)), (76, (1, 1))])
+def test_i8_conv_window_path_general_geometry(ctx, layout, wd, pad):
     """The LDS-window conv kernel (group 1, IC % 64 == 0) on a ragged shape: OC not a multiple of 64,
-    asymmetric stride/pad/dilation, non-zero input zero point, output width not a multiple of 32."""
+    asymmetric stride/pad/dilation, non-zero input zero point, output width not a multiple of 32.
+    Width 23 stages NCHW rows byte by byte; width 76 (rows 4-byte aligned, odd left pad, two blocks per
+    output row) takes the aligned-dword staging with a 3-byte shift."""
     r = rng(41)
-    n, c, h, wd, oc = 2, 128, 17, 23, 80
+    n, c, h, oc = 2, 128, 17, 80
     x = r.integers(-128, 128, (n, c, h, wd)).astype(np.int8)
     w = r.integers(-127, 128, (oc, c, 3, 3)).astype(np.int8)
     s_w = r.uniform(1e-3, 1e-2, oc).astype(np.float32)
     bias = r.integers(-3000, 3000, oc).astype(np.int32)
     xl = x if layout == 0 else np.ascontiguousarray(x.transpose(0, 2, 3, 1))
-    rc, ref = po.i8_conv2d(xl, 0.03, -5, w, s_w, bias, (1, 2), (1, 0), 0.05, 2, dilation=(2, 1), layout=layout)
+    rc, ref = po.i8_conv2d(xl, 0.03, -5, w, s_w, bias, (1, 2), pad, 0.05, 2, dilation=(2, 1), layout=layout)
     assert rc == 0
     wt = ctx.prepare_conv_weight(dev(w), s_w, version=6)
     out = torch.empty(ref.shape, dtype=torch.int8, device="cuda")
-    ctx.i8_conv2d(dev(xl), layout, 0.03, -5, wt, out, 0.05, 2, stride=(1, 2), pad=(1, 0), dilation=(2, 1),
+    ctx.i8_conv2d(dev(xl), layout, 0.03, -5, wt, out, 0.05, 2, stride=(1, 2), pad=pad, dilation=(2, 1),
                   bias=dev(bias), bias_abs_max=3000)
     assert ctx.last_backend() == "i8_mfma_conv_window"
     got = out.cpu().numpy()
