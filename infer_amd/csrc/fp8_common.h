@@ -85,6 +85,50 @@ struct Fp8Epilogue {
     }
 };
 
+// Reference code for a value the hardware converter cannot encode the reference's way: beyond the
+// largest finite code the reference saturates finite overflow to max finite, and maps Inf to 0x7e
+// (e4m3) / 0x7c (e5m2) and NaN to 0x7f / 0x7d, each with the value's sign (include/util/fp8.h:66-211).
+// In-range values keep the hardware's round-to-nearest-even code.
+template <bool E5>
+__device__ __forceinline__ uint32_t fixup_code(float q, uint32_t hw_code) {
+    const uint32_t bits = __float_as_uint(q);
+    const uint32_t mag = bits & 0x7fffffffu;
+    const uint32_t sign = (bits >> 24) & 0x80u;
+    const uint32_t special = mag > 0x7f800000u ? (E5 ? 0x7du : 0x7fu)
+                                                : (mag == 0x7f800000u ? (E5 ? 0x7cu : 0x7eu) : (E5 ? 0x7bu : 0x7eu));
+    return mag <= (E5 ? 0x47600000u : 0x43e00000u) ? hw_code : (sign | special);
+}
+
+template <bool E5>
+__device__ __forceinline__ float decode_code(uint32_t code) {
+    const v2f d = E5 ? __builtin_amdgcn_cvt_pk_f32_bf8((int)code, false) : __builtin_amdgcn_cvt_pk_f32_fp8((int)code, false);
+    return (d.x != d.x) ? __uint_as_float(0x7fc00000u) : d.x;  // the reference decodes NaN codes to +qNaN
+}
+
+// Four values -> four FP8 codes packed little-endian: hardware converter for finite in-range values,
+// reference saturated / special codes otherwise (NaN fails every comparison and takes the fix-up).
+template <bool E5>
+__device__ __forceinline__ uint32_t encode4(const float (&q)[4]) {
+    int pk = E5 ? __builtin_amdgcn_cvt_pk_bf8_f32(q[0], q[1], 0, false) : __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+    pk = E5 ? __builtin_amdgcn_cvt_pk_bf8_f32(q[2], q[3], pk, true) : __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], pk, true);
+    const float maxf = E5 ? 57344.0f : 448.0f;
+    uint32_t packed = (uint32_t)pk;
+    const bool in_range = __builtin_fabsf(q[0]) <= maxf && __builtin_fabsf(q[1]) <= maxf &&
+                          __builtin_fabsf(q[2]) <= maxf && __builtin_fabsf(q[3]) <= maxf;
+    if (__builtin_expect(!in_range, 0)) {
+        packed = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) packed |= fixup_code<E5>(q[t], ((uint32_t)pk >> (8 * t)) & 0xffu) << (8 * t);
+    }
+    return packed;
+}
+
+template <bool E5>
+__device__ __forceinline__ uint32_t encode1(float q) {
+    const int pk = E5 ? __builtin_amdgcn_cvt_pk_bf8_f32(q, 0.0f, 0, false) : __builtin_amdgcn_cvt_pk_fp8_f32(q, 0.0f, 0, false);
+    return fixup_code<E5>(q, (uint32_t)pk & 0xffu);
+}
+
 constexpr int kGemvThreads = 256;
 constexpr int kGemvMaxLds = 64 * 1024;
 #ifndef FHIP_GEMV_R1

@@ -109,22 +109,6 @@ __device__ __forceinline__ float scaled(const Fp8Epilogue& ep, float mul, float 
     }
 }
 
-template <bool E5>
-__device__ __forceinline__ uint32_t fixup_code(float q, uint32_t hw_code) {
-    const uint32_t bits = __float_as_uint(q);
-    const uint32_t mag = bits & 0x7fffffffu;
-    const uint32_t sign = (bits >> 24) & 0x80u;
-    const uint32_t special = mag > 0x7f800000u ? (E5 ? 0x7du : 0x7fu)
-                                                : (mag == 0x7f800000u ? (E5 ? 0x7cu : 0x7eu) : (E5 ? 0x7bu : 0x7eu));
-    return mag <= (E5 ? 0x47600000u : 0x43e00000u) ? hw_code : (sign | special);
-}
-
-template <bool E5>
-__device__ __forceinline__ float decode_code(uint32_t code) {
-    const v2f d = E5 ? __builtin_amdgcn_cvt_pk_f32_bf8((int)code, false) : __builtin_amdgcn_cvt_pk_f32_fp8((int)code, false);
-    return (d.x != d.x) ? __uint_as_float(0x7fc00000u) : d.x;  // the reference decodes NaN codes to +qNaN
-}
-
 // Output bits of four consecutive columns (col..col+3) of one row, packed little-endian: four FP8 codes
 // in one dword (OUT_BYTES 1), four BF16 in two dwords (2) or four FP32 (4).  The hardware converter
 // encodes finite in-range values (round to nearest even; checked against the reference codec on every
@@ -137,18 +121,7 @@ __device__ __forceinline__ void fast_value4(const Fp8Epilogue& ep, float mul, co
     float q[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) q[t] = scaled<E5, POW2, BIAS>(ep, mul, acc[t], row, col + t);
-    int pk = E5 ? __builtin_amdgcn_cvt_pk_bf8_f32(q[0], q[1], 0, false) : __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
-    pk = E5 ? __builtin_amdgcn_cvt_pk_bf8_f32(q[2], q[3], pk, true) : __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], pk, true);
-    const float maxf = E5 ? 57344.0f : 448.0f;
-    uint32_t packed = (uint32_t)pk;
-    // NaN fails every comparison, so it also takes the fix-up path.
-    const bool in_range = __builtin_fabsf(q[0]) <= maxf && __builtin_fabsf(q[1]) <= maxf &&
-                          __builtin_fabsf(q[2]) <= maxf && __builtin_fabsf(q[3]) <= maxf;
-    if (__builtin_expect(!in_range, 0)) {
-        packed = 0;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) packed |= fixup_code<E5>(q[t], ((uint32_t)pk >> (8 * t)) & 0xffu) << (8 * t);
-    }
+    const uint32_t packed = encode4<E5>(q);
     if constexpr (OUT_BYTES == 1) {
         out[0] = packed;
     } else {

@@ -43,39 +43,51 @@ __device__ __forceinline__ uint8_t encode_act(uint32_t bits, float a_scale, floa
     return fhip::fp8_encode(scale_down(x, a_scale, a_inv), E5);
 }
 
-template <bool E5, int ADT>
+// `after_first_loads` runs once, right after the first batch of activation loads is issued: the caller
+// issues its weight stream there, so the (in-order) wait for the activations does not also wait for it.
+template <bool E5, int ADT, int MT, class F>
 __device__ __forceinline__ void stage_activations(const void* __restrict__ a, int a_vec, float a_scale, float a_inv,
-                                                  int64_t m, int64_t k, int64_t kp, int mt, uint8_t* xs, int tid) {
-    constexpr int kBatch = 4;
+                                                  int64_t m, int64_t k, int64_t kp, int mt, uint8_t* xs, int tid,
+                                                  F&& after_first_loads) {
+    bool first = true;
+    constexpr int kBatch = MT == 1 ? 1 : 4;  // one row of up to 1024 codes is one group per thread
     constexpr int esz = ADT == 0 ? 1 : (ADT == 1 ? 2 : 4);
     const int64_t groups = (int64_t)mt * kp / 4;
     const int64_t gpr = kp / 4;  // groups per row
     if (a_vec) {
         for (int64_t g0 = tid; g0 < groups; g0 += (int64_t)kGemvThreads * kBatch) {
             uint32_t raw[kBatch][4];
+            // Loads are unconditional (out-of-range groups read element 0 and are masked afterwards), so
+            // the batch issues back to back and costs one memory round trip.
 #pragma unroll
             for (int u = 0; u < kBatch; ++u) {
                 const int64_t g = g0 + (int64_t)u * kGemvThreads;
                 const int64_t r = g / gpr, kk = (g - r * gpr) * 4;
-                raw[u][0] = raw[u][1] = raw[u][2] = raw[u][3] = 0u;
-                if (g < groups && r < m && kk < k) {
-                    const uint8_t* src = static_cast<const uint8_t*>(a) + (r * k + kk) * esz;
-                    if constexpr (ADT == 0) {
-                        raw[u][0] = *reinterpret_cast<const uint32_t*>(src);
-                    } else if constexpr (ADT == 1) {
-                        const uint2 v = *reinterpret_cast<const uint2*>(src);
-                        raw[u][0] = v.x & 0xffffu;
-                        raw[u][1] = v.x >> 16;
-                        raw[u][2] = v.y & 0xffffu;
-                        raw[u][3] = v.y >> 16;
-                    } else {
-                        const uint4 v = *reinterpret_cast<const uint4*>(src);
-                        raw[u][0] = v.x;
-                        raw[u][1] = v.y;
-                        raw[u][2] = v.z;
-                        raw[u][3] = v.w;
-                    }
+                const bool live = g < groups && r < m && kk < k;
+                const uint8_t* src = static_cast<const uint8_t*>(a) + (live ? (r * k + kk) * esz : 0);
+                uint32_t v4[4];
+                if constexpr (ADT == 0) {
+                    v4[0] = *reinterpret_cast<const uint32_t*>(src);
+                    v4[1] = v4[2] = v4[3] = 0u;
+                } else if constexpr (ADT == 1) {
+                    const uint2 v = *reinterpret_cast<const uint2*>(src);
+                    v4[0] = v.x & 0xffffu;
+                    v4[1] = v.x >> 16;
+                    v4[2] = v.y & 0xffffu;
+                    v4[3] = v.y >> 16;
+                } else {
+                    const uint4 v = *reinterpret_cast<const uint4*>(src);
+                    v4[0] = v.x;
+                    v4[1] = v.y;
+                    v4[2] = v.z;
+                    v4[3] = v.w;
                 }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) raw[u][i] = live ? v4[i] : 0u;
+            }
+            if (first) {
+                after_first_loads();
+                first = false;
             }
 #pragma unroll
             for (int u = 0; u < kBatch; ++u) {
@@ -94,6 +106,7 @@ __device__ __forceinline__ void stage_activations(const void* __restrict__ a, in
             }
         }
     } else {
+        after_first_loads();
         for (int64_t idx = tid; idx < (int64_t)mt * kp; idx += kGemvThreads) {
             const int64_t r = idx / kp, kk = idx - r * kp;
             uint8_t code = 0;
@@ -124,11 +137,13 @@ __global__ __launch_bounds__(kGemvThreads) void fp8_gemv_kernel(const void* __re
     const int64_t chunks = kp / 16;
     // Rows past n stay inside the zero-padded prepared weight (Np is a multiple of 256).
     uint4 wv[R];
-    if (lane < chunks) {
+    stage_activations<E5, ADT, MT>(a, a_vec, a_scale, a_inv, m, k, kp, MT, xs, tid, [&] {
+        // unconditional (lanes past a short row re-read its last chunk and ignore it), so the compiler
+        // can count these loads exactly when it waits for the activations
+        const int64_t c0 = lane < chunks ? lane : chunks - 1;
 #pragma unroll
-        for (int r = 0; r < R; ++r) wv[r] = load_stream16(w + (row0 + r) * kp + lane * 16);
-    }
-    stage_activations<E5, ADT>(a, a_vec, a_scale, a_inv, m, k, kp, MT, xs, tid);
+        for (int r = 0; r < R; ++r) wv[r] = load_stream16(w + (row0 + r) * kp + c0 * 16);
+    });
     __syncthreads();
 
     float acc[R][MT];
@@ -180,6 +195,126 @@ __global__ __launch_bounds__(kGemvThreads) void fp8_gemv_kernel(const void* __re
         for (int j = 0; j < MT; ++j) {
             if (lane == r * MT + j && j < m && row0 + r < n) ep.store(acc[r][j], j, row0 + r);
         }
+}
+
+// ---- M = 1 decode GEMV, the common case ---------------------------------------------------------
+// One activation row whose elements come in aligned groups of 4, power-of-two activation and output
+// scales (so x / s is x * (1/s) exactly) -- the fused Cast -> MatMul -> Cast of decoding.  Same
+// arithmetic as fp8_gemv_kernel, with everything the general kernel decides at run time fixed at
+// compile time: the activation load is issued first (an L2 hit, so its wait does not also wait for
+// the weight stream issued right after), encoding is the hardware converter with the reference's
+// saturation fix-up, and the output type is a template parameter.
+template <int ADT>
+__device__ __forceinline__ void load_act_group(const void* __restrict__ a, int64_t k, int g, float a_inv,
+                                               uint32_t (&raw)[4], bool& live) {
+    live = (int64_t)g * 4 < k;
+    const int64_t e = live ? (int64_t)g * 4 : 0;
+    if constexpr (ADT == 0) {
+        raw[0] = *(reinterpret_cast<const uint32_t*>(a) + e / 4);
+    } else if constexpr (ADT == 1) {
+        const uint2 v = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a) + e);
+        raw[0] = v.x << 16;
+        raw[1] = v.x & 0xffff0000u;
+        raw[2] = v.y << 16;
+        raw[3] = v.y & 0xffff0000u;
+    } else {
+        const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const float*>(a) + e);
+        raw[0] = v.x;
+        raw[1] = v.y;
+        raw[2] = v.z;
+        raw[3] = v.w;
+    }
+}
+
+template <bool E5, int ADT>
+__device__ __forceinline__ uint32_t encode_act_group(const uint32_t (&raw)[4], float a_inv, bool live) {
+    if (!live) return 0u;
+    if constexpr (ADT == 0) return raw[0];
+    float q[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = fhip::bits_f32(raw[i]) * a_inv;
+    return encode4<E5>(q);
+}
+
+template <bool E5, int ADT, int OUT_BYTES, int R>
+__global__ __launch_bounds__(kGemvThreads) void fp8_gemv1_kernel(const void* __restrict__ a, float a_inv, int64_t k,
+                                                                  const uint8_t* __restrict__ w, int64_t kp, int64_t n,
+                                                                  Fp8Epilogue ep) {
+    extern __shared__ __align__(16) uint8_t xs[];  // [kp] FP8 codes
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int64_t row0 = ((int64_t)blockIdx.x * (kGemvThreads / 64) + wave) * R;
+    const int groups = (int)(kp / 4);
+    const int chunks = (int)(kp / 16);
+
+    uint32_t raw[4];
+    bool live;
+    load_act_group<ADT>(a, k, tid < groups ? tid : 0, a_inv, raw, live);
+    live = live && tid < groups;
+    uint4 wv[R];
+    {
+        const int c0 = lane < chunks ? lane : chunks - 1;  // lanes past a short row re-read its last chunk
+#pragma unroll
+        for (int r = 0; r < R; ++r) wv[r] = load_stream16(w + (row0 + r) * kp + c0 * 16);
+    }
+    if (tid < groups) *reinterpret_cast<uint32_t*>(xs + tid * 4) = encode_act_group<E5, ADT>(raw, a_inv, live);
+    for (int g = tid + kGemvThreads; g < groups; g += kGemvThreads) {  // rows longer than 1024
+        load_act_group<ADT>(a, k, g, a_inv, raw, live);
+        *reinterpret_cast<uint32_t*>(xs + g * 4) = encode_act_group<E5, ADT>(raw, a_inv, live);
+    }
+    __syncthreads();
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    for (int c = lane; c < chunks; c += 64) {
+        if (c != lane) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) wv[r] = load_stream16(w + (row0 + r) * kp + c * 16);
+        }
+        const uint4 xv = *reinterpret_cast<const uint4*>(xs + c * 16);
+        float xf[16];
+        decode4<E5>(xv.x, xf);
+        decode4<E5>(xv.y, xf + 4);
+        decode4<E5>(xv.z, xf + 8);
+        decode4<E5>(xv.w, xf + 12);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float wf[16];
+            decode4<E5>(wv[r].x, wf);
+            decode4<E5>(wv[r].y, wf + 4);
+            decode4<E5>(wv[r].z, wf + 8);
+            decode4<E5>(wv[r].w, wf + 12);
+            float s = acc[r];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s += wf[i] * xf[i];
+            acc[r] = s;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = fhip::wave_sum(acc[r]);
+    float mine = acc[0];
+#pragma unroll
+    for (int r = 1; r < R; ++r) mine = lane == r ? acc[r] : mine;
+    const int64_t col = row0 + lane;
+    if (lane < R && col < n) {
+        // the general epilogue's order: acc*ab_scale, *alpha, [+ beta*bias], then * (1/out_scale)
+        float y = mine * ep.ab_scale;
+        y *= ep.alpha;
+        if (ep.bias_kind != FHIP_BIAS_NONE) {
+            const uint8_t bc = ep.bias[col];  // vector bias (a matrix bias has one row here)
+            y += ep.beta * (fhip::fp8_decode(bc, E5) * ep.bias_scale);
+        }
+        const uint32_t code = encode1<E5>(y * ep.out_inv);
+        if constexpr (OUT_BYTES == 1) {
+            static_cast<uint8_t*>(ep.out)[col] = (uint8_t)code;
+        } else if constexpr (OUT_BYTES == 2) {
+            static_cast<uint16_t*>(ep.out)[col] = fhip::bf16_encode(decode_code<E5>(code) * ep.out_scale);
+        } else {
+            static_cast<float*>(ep.out)[col] = decode_code<E5>(code) * ep.out_scale;
+        }
+    }
 }
 
 // ---- GEMM operand staging: FP8 codes [m][k64], k64 = k rounded up to 64, zero padded; BF16/FP32
@@ -251,6 +386,20 @@ int launch_gemv_t(fhip_context ctx, const void* a, float a_scale, int64_t m, con
     const uint8_t* wd = static_cast<const uint8_t*>(w->data);
     const int a_vec = (w->k % 4 == 0 && (reinterpret_cast<uintptr_t>(a) & 15) == 0) ? 1 : 0;
     const float a_inv = pow2_inverse(a_scale);
+    if (m == 1 && a_vec && a_inv != 0.0f && ep.out_inv != 0.0f) {
+        constexpr int R = FHIP_GEMV_R1;
+        const unsigned grid = (unsigned)((w->n + 4 * R - 1) / (4 * R));
+        const size_t lds = (size_t)kp;
+        if (ep.out_dtype == FHIP_BF16)
+            fp8_gemv1_kernel<E5, ADT, 2, R><<<grid, kGemvThreads, lds, ctx->stream>>>(a, a_inv, w->k, wd, kp, w->n, ep);
+        else if (ep.out_dtype == FHIP_FP32)
+            fp8_gemv1_kernel<E5, ADT, 4, R><<<grid, kGemvThreads, lds, ctx->stream>>>(a, a_inv, w->k, wd, kp, w->n, ep);
+        else
+            fp8_gemv1_kernel<E5, ADT, 1, R><<<grid, kGemvThreads, lds, ctx->stream>>>(a, a_inv, w->k, wd, kp, w->n, ep);
+        ctx->last_backend = "fp8_gemv_m1";
+        FHIP_CHECK_LAUNCH(ctx, "fp8_gemv1_kernel");
+        return FHIP_OK;
+    }
 #define FHIP_GEMV_CASE(MT, R)                                                                                       \
     if (m <= MT) {                                                                                                  \
         const unsigned grid = (unsigned)((w->n + 4 * R - 1) / (4 * R));                                             \

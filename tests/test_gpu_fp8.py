@@ -89,9 +89,10 @@ def test_fp8_gemv_matches_oracle(ctx, dtype, m, layout):
 
 
 @pytest.mark.parametrize("dtype", FP8)
-def test_fp8_gemv_fused_bf16_io(ctx, dtype):
+@pytest.mark.parametrize("m", [1, 4])
+def test_fp8_gemv_fused_bf16_io(ctx, dtype, m):
     """bf16 activations -> Cast(fp8) -> MatMul -> Cast(bf16), fused: equals the three-node chain."""
-    m, k, n = 4, 1024, 3584
+    k, n = 1024, 3584
     r = rng(SEEDS[2])
     x = r.standard_normal((m, k)).astype(np.float32)
     xb = po.bf16_encode(x)
@@ -134,6 +135,50 @@ def test_fp8_mfma_gemm_matches_oracle(ctx, dtype, shape):
     wt.release()
 
 
+def _encode_probe_values(dtype, count, seed):
+    """Activation values (in units of the activation scale) that exercise the FP8 encode: every finite
+    code's value, the midpoints between neighbouring codes (round-half-even ties), values past the
+    largest finite code (saturation), subnormal-range and sub-subnormal magnitudes, both zeros."""
+    codes = np.arange(256, dtype=np.uint8)
+    vals = po.fp8_decode(dtype, codes).astype(np.float64)
+    fin = np.sort(np.unique(vals[np.isfinite(vals) & (vals >= 0)]))
+    mids = (fin[:-1] + fin[1:]) / 2
+    maxf = fin[-1]
+    extra = np.array([maxf * 1.01, maxf * 1.2, maxf * 4, fin[1] / 2, fin[1] / 3, fin[1] / 2 * 1.0001, 0.0])
+    pos = np.concatenate([fin, mids, extra])
+    v = np.concatenate([pos, -pos, [-0.0]])
+    r = rng(seed)
+    v = np.concatenate([v, r.standard_normal(count) * maxf / 4])[:count]
+    return r.permutation(v).astype(np.float32)
+
+
+@pytest.mark.parametrize("dtype", FP8)
+@pytest.mark.parametrize("src", [po.FP32, po.BF16])
+def test_fp8_gemv_m1_activation_encode_exact(ctx, dtype, src):
+    """With an identity weight (code of 1.0 on the diagonal, w_scale 1) and out_scale = a_scale, every
+    output code equals the activation's own Cast code, so the fused encode inside the M=1 kernel is
+    checked bit-exactly against the reference Cast.  K = N = 1088 (padded 1152) makes the kernel stage
+    the row in two passes and walk the weight row in two chunks per lane."""
+    k = n = 1088
+    s_in = 0.25
+    v = _encode_probe_values(dtype, k, 31)
+    x = (v * np.float32(s_in)).astype(np.float32).reshape(1, k)
+    xin = x if src == po.FP32 else po.bf16_encode(x)
+    one = int(po.fp8_encode(dtype, np.array([1.0], np.float32))[0])
+    w = np.zeros((k, n), np.uint8)
+    w[np.arange(k), np.arange(n)] = one
+    wt = ctx.prepare_weight(dev(w), dtype, k, n, 0, version=6)
+    out = torch.empty((1, n), dtype=torch.uint8, device="cuda")
+    ctx.fp8_linear(dev(xin), src, s_in, 1, wt, 1.0, out, dtype, s_in)
+    assert ctx.last_backend() == "fp8_gemv_m1"
+    a_codes = po.cast_to_fp8(src, xin, dtype, s_in)
+    ref = po.fp8_matmul(dtype, a_codes, s_in, w, 1.0, s_in)
+    got = host(out)
+    bad = np.nonzero(got != ref)[1]
+    assert bad.size == 0, f"{bad.size} mismatches: x={x[0, bad[:4]]} got={got[0, bad[:4]]} ref={ref[0, bad[:4]]}"
+    wt.release()
+
+
 def test_fp8_gemm_bias_alpha_beta(ctx):
     dtype = po.FP8E4M3
     m, k, n = 64, 256, 96
@@ -141,7 +186,7 @@ def test_fp8_gemm_bias_alpha_beta(ctx):
     bias_f = rng(12).standard_normal(n).astype(np.float32) * 0.1
     bias, sb = fp8_tensor(bias_f, dtype)
     wt = ctx.prepare_weight(dev(w_src), dtype, k, n, 1, version=4)
-    for mm in (m, 8):
+    for mm in (m, 8, 1):
         out = torch.empty((mm, n), dtype=torch.uint8, device="cuda")
         ctx.fp8_linear(dev(a[:mm]), dtype, sa, mm, wt, sw, out, dtype, s_out, bias=dev(bias), bias_scale=sb,
                        bias_kind=po.BIAS_VECTOR, alpha=0.5, beta=2.0)
