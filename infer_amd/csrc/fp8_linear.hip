@@ -9,9 +9,11 @@
 // K-ordered fp32 sum only by accumulation order (<= 1 FP8 code after the output encode).
 //
 // Two paths:
-//   * fp8_gemv_kernel   -- decode rows (m <= 16): bandwidth-bound.  Weight rows stream from HBM
-//                          with 16-byte loads, activations are staged once per block in LDS as FP8
-//                          codes, products accumulate on the VALU, a cross-lane butterfly reduces.
+//   * fp8_gemv1_kernel  -- one decode row with power-of-two scales (the fused Cast -> MatMul -> Cast):
+//                          bandwidth-bound; weight rows stream with 16-byte loads, products accumulate
+//                          on the VALU, a cross-lane butterfly reduces.
+//   * fp8_gemv_mfma_kernel -- any m <= 16: weight columns straight from HBM as MFMA B operands,
+//                          activations staged once per block in LDS as FP8 codes.
 //   * fp8_gemm_kernel (fp8_gemm.hip) -- prefill (m > 16): MFMA, fp32 accumulation.
 // Weights come prepared as [Np][Kp] (K contiguous, zero padded; runtime.hip).
 #include "fp8_common.h"
@@ -97,10 +99,12 @@ __device__ __forceinline__ void stage_activations(const void* __restrict__ a, in
                 if constexpr (ADT == 0) {
                     c = raw[u][0];
                 } else {
-                    c = (uint32_t)encode_act<E5, ADT>(raw[u][0], a_scale, a_inv) |
-                        ((uint32_t)encode_act<E5, ADT>(raw[u][1], a_scale, a_inv) << 8) |
-                        ((uint32_t)encode_act<E5, ADT>(raw[u][2], a_scale, a_inv) << 16) |
-                        ((uint32_t)encode_act<E5, ADT>(raw[u][3], a_scale, a_inv) << 24);
+                    float q[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        q[i] = scale_down(ADT == 1 ? fhip::bits_f32(raw[u][i] << 16) : fhip::bits_f32(raw[u][i]),
+                                          a_scale, a_inv);
+                    c = encode4<E5>(q);
                 }
                 *reinterpret_cast<uint32_t*>(xs + g * 4) = c;
             }
@@ -121,80 +125,72 @@ __device__ __forceinline__ void stage_activations(const void* __restrict__ a, in
     }
 }
 
-// grid.x = ceil(n / (4 waves * R rows)); one wave owns R weight rows, lane l owns the 16-byte
-// chunks l, l+64, ... of each row.  The first chunk of every row is requested before the block
-// stages its activations, so the weight stream and the activation staging overlap (one HBM round
-// trip for K <= 1024 instead of two).
-template <bool E5, int MT, int R, int ADT>
-__global__ __launch_bounds__(kGemvThreads) void fp8_gemv_kernel(const void* __restrict__ a, int a_vec, float a_scale, float a_inv,
-                                                                 int64_t m, int64_t k, const uint8_t* __restrict__ w,
-                                                                 int64_t kp, int64_t n, Fp8Epilogue ep) {
-    extern __shared__ __align__(16) uint8_t xs[];  // [MT][kp] FP8 codes
+// ---- Decode GEMV on MFMA (any m <= 16) -----------------------------------------------------------
+// A block owns 16 output columns; its 4 waves split K (wave w takes the 128-deep steps w, w+4, ...).
+// v_mfma_scale_f32_16x16x128_f8f6f4 with unit scales multiplies the activation rows (A, staged as FP8
+// codes in LDS, rows >= m zero) by the weight columns (B, straight from HBM into registers): no
+// per-element decode, and the MFMA does the K reduction inside each step.  Lane l supplies row/column
+// l%16 and the 32-byte K slice l/16 of the step, for A and B alike.  The four partial 16x16 tiles are
+// summed through LDS and every thread finishes one output.  The first batch of weight loads is issued
+// right after the activation loads, so the weight stream and the staging overlap.
+constexpr int kGemvUnroll = 4;  // steps per wave whose weight loads are in flight together
+
+template <bool E5, int ADT>
+__global__ __launch_bounds__(kGemvThreads) void fp8_gemv_mfma_kernel(const void* __restrict__ a, int a_vec,
+                                                                      float a_scale, float a_inv, int64_t m, int64_t k,
+                                                                      const uint8_t* __restrict__ w, int64_t kp,
+                                                                      int64_t n, Fp8Epilogue ep) {
+    extern __shared__ __align__(16) uint8_t xs[];  // [m][kp] FP8 codes
+    __shared__ float red[4][16][17];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int64_t row0 = ((int64_t)blockIdx.x * (kGemvThreads / 64) + wave) * R;
-    const int64_t chunks = kp / 16;
-    // Rows past n stay inside the zero-padded prepared weight (Np is a multiple of 256).
-    uint4 wv[R];
-    stage_activations<E5, ADT, MT>(a, a_vec, a_scale, a_inv, m, k, kp, MT, xs, tid, [&] {
-        // unconditional (lanes past a short row re-read its last chunk and ignore it), so the compiler
-        // can count these loads exactly when it waits for the activations
-        const int64_t c0 = lane < chunks ? lane : chunks - 1;
+    const int64_t col0 = (int64_t)blockIdx.x * 16;
+    const int steps = (int)(kp / 128);
+    const int fr = lane & 15;
+    const int fq = lane >> 4;
+    const uint8_t* wcol = w + (col0 + fr) * kp + fq * 32;  // rows past n: zero padding of the prepared weight
+    uint4 wb[kGemvUnroll][2];
+    auto load_batch = [&](int s0) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) wv[r] = load_stream16(w + (row0 + r) * kp + c0 * 16);
-    });
+        for (int u = 0; u < kGemvUnroll; ++u) {
+            const int s = s0 + 4 * u;
+            const uint8_t* p = wcol + (int64_t)(s < steps ? s : steps - 1) * 128;  // clamped: unconditional
+            wb[u][0] = load_stream16(p);
+            wb[u][1] = load_stream16(p + 16);
+        }
+    };
+    stage_activations<E5, ADT, 16>(a, a_vec, a_scale, a_inv, m, k, kp, (int)m, xs, tid, [&] { load_batch(wave); });
     __syncthreads();
 
-    float acc[R][MT];
+    const int fmt = E5 ? 1 : 0;
+    const bool arow = fr < m;
+    const uint8_t* xrow = xs + (arow ? fr : 0) * kp + fq * 32;
+    v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = wave; s0 < steps; s0 += 4 * kGemvUnroll) {
+        if (s0 != wave) load_batch(s0);
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int j = 0; j < MT; ++j) acc[r][j] = 0.0f;
-
-    for (int64_t c = lane; c < chunks; c += 64) {
-        if (c != lane) {
-#pragma unroll
-            for (int r = 0; r < R; ++r) wv[r] = load_stream16(w + (row0 + r) * kp + c * 16);
-        }
-        float wf[R][16];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            decode4<E5>(wv[r].x, wf[r]);
-            decode4<E5>(wv[r].y, wf[r] + 4);
-            decode4<E5>(wv[r].z, wf[r] + 8);
-            decode4<E5>(wv[r].w, wf[r] + 12);
-        }
-#pragma unroll
-        for (int j = 0; j < MT; ++j) {
-            const uint4 xv = *reinterpret_cast<const uint4*>(xs + j * kp + c * 16);
-            float xf[16];
-            decode4<E5>(xv.x, xf);
-            decode4<E5>(xv.y, xf + 4);
-            decode4<E5>(xv.z, xf + 8);
-            decode4<E5>(xv.w, xf + 12);
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                float s = acc[r][j];
-#pragma unroll
-                for (int i = 0; i < 16; ++i) s += wf[r][i] * xf[i];
-                acc[r][j] = s;
+        for (int u = 0; u < kGemvUnroll; ++u) {
+            const int s = s0 + 4 * u;
+            if (s >= steps) break;  // wave-uniform
+            uint4 x0 = make_uint4(0, 0, 0, 0), x1 = x0;
+            if (arow) {
+                x0 = *reinterpret_cast<const uint4*>(xrow + s * 128);
+                x1 = *reinterpret_cast<const uint4*>(xrow + s * 128 + 16);
             }
+            const v8i av = v8i{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+            const v8i bv = v8i{(int)wb[u][0].x, (int)wb[u][0].y, (int)wb[u][0].z, (int)wb[u][0].w,
+                               (int)wb[u][1].x, (int)wb[u][1].y, (int)wb[u][1].z, (int)wb[u][1].w};
+            acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc, fmt, fmt, 0, 127, 0, 127);
         }
     }
-    // Butterfly over the 64 lanes: every lane ends with the full sums.
+    // C fragment of lane l: column l%16, rows 4*(l/16) .. +3.
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int j = 0; j < MT; ++j) {
-            acc[r][j] = fhip::wave_sum(acc[r][j]);
-        }
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int j = 0; j < MT; ++j) {
-            if (lane == r * MT + j && j < m && row0 + r < n) ep.store(acc[r][j], j, row0 + r);
-        }
+    for (int r = 0; r < 4; ++r) red[wave][fq * 4 + r][fr] = acc[r];
+    __syncthreads();
+    const int row = tid >> 4, cc = tid & 15;
+    const int64_t col = col0 + cc;
+    if (row < m && col < n) ep.store(red[0][row][cc] + red[1][row][cc] + red[2][row][cc] + red[3][row][cc], row, col);
 }
 
 // ---- M = 1 decode GEMV, the common case ---------------------------------------------------------
@@ -378,7 +374,6 @@ unsigned grid_for(int64_t count, int threads) {
     return (unsigned)(blocks < 1 ? 1 : blocks);
 }
 
-// Rows per wave: small m streams more rows per wave to keep more bytes in flight per lane.
 template <bool E5, int ADT>
 int launch_gemv_t(fhip_context ctx, const void* a, float a_scale, int64_t m, const fhip_weight_s* w,
                   const Fp8Epilogue& ep) {
@@ -400,22 +395,15 @@ int launch_gemv_t(fhip_context ctx, const void* a, float a_scale, int64_t m, con
         FHIP_CHECK_LAUNCH(ctx, "fp8_gemv1_kernel");
         return FHIP_OK;
     }
-#define FHIP_GEMV_CASE(MT, R)                                                                                       \
-    if (m <= MT) {                                                                                                  \
-        const unsigned grid = (unsigned)((w->n + 4 * R - 1) / (4 * R));                                             \
-        const size_t lds = (size_t)MT * kp;                                                                         \
-        fp8_gemv_kernel<E5, MT, R, ADT><<<grid, kGemvThreads, lds, ctx->stream>>>(a, a_vec, a_scale, a_inv, m, w->k, wd,   \
-                                                                                  kp, w->n, ep);                    \
-        ctx->last_backend = "fp8_gemv_m" #MT;                                                                      \
-        FHIP_CHECK_LAUNCH(ctx, "fp8_gemv_kernel");                                                                  \
-        return FHIP_OK;                                                                                             \
+    if (m <= 16) {
+        const unsigned grid = (unsigned)((w->n + 15) / 16);
+        const size_t lds = (size_t)m * kp;
+        fp8_gemv_mfma_kernel<E5, ADT><<<grid, kGemvThreads, lds, ctx->stream>>>(a, a_vec, a_scale, a_inv, m, w->k, wd,
+                                                                               kp, w->n, ep);
+        ctx->last_backend = "fp8_gemv_mfma";
+        FHIP_CHECK_LAUNCH(ctx, "fp8_gemv_mfma_kernel");
+        return FHIP_OK;
     }
-    FHIP_GEMV_CASE(1, FHIP_GEMV_R1)
-    FHIP_GEMV_CASE(2, 2)
-    FHIP_GEMV_CASE(4, 2)
-    FHIP_GEMV_CASE(8, 2)
-    FHIP_GEMV_CASE(16, 2)
-#undef FHIP_GEMV_CASE
     return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "gemv: m > 16");
 }
 

@@ -89,6 +89,23 @@ def test_fp8_gemv_matches_oracle(ctx, dtype, m, layout):
 
 
 @pytest.mark.parametrize("dtype", FP8)
+@pytest.mark.parametrize("m", [1, 5, 16])
+def test_fp8_gemv_long_k_non_pow2_scale(ctx, dtype, m):
+    """Down-projection shape (K = 3584: 28 MFMA steps, so each wave runs two load batches) with a
+    non-power-of-two output scale, which takes the general MFMA GEMV at every m (including m = 1)."""
+    k, n = 3584, 1024
+    a, sa, w_nk, w_src, sw, s_out = _linear_case(SEEDS[2] + 100 + m, dtype, m, k, n, 1)
+    s_out = float(np.float32(s_out * 1.37))
+    wt = ctx.prepare_weight(dev(w_src), dtype, k, n, 1, version=7)
+    out = torch.empty((m, n), dtype=torch.uint8, device="cuda")
+    ctx.fp8_linear(dev(a), dtype, sa, m, wt, sw, out, dtype, s_out)
+    assert ctx.last_backend() == "fp8_gemv_mfma"
+    ref = po.fp8_gemm(dtype, a, sa, w_nk, sw, True, s_out)
+    fp8_linear_check(dtype, host(out), ref, a, sa, w_nk, sw, s_out, f"gemv long k m={m}")
+    wt.release()
+
+
+@pytest.mark.parametrize("dtype", FP8)
 @pytest.mark.parametrize("m", [1, 4])
 def test_fp8_gemv_fused_bf16_io(ctx, dtype, m):
     """bf16 activations -> Cast(fp8) -> MatMul -> Cast(bf16), fused: equals the three-node chain."""
