@@ -23,6 +23,9 @@ namespace {
 
 typedef float v2f __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ uint4 load_stream16(const uint8_t* p) {
     const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
@@ -92,6 +95,45 @@ struct HeadParams {
     float out_scale;  // FP8: output scale
     float* logits;    // optional [m][v]
 };
+
+// Publishes nothing itself: called by every block after it wrote its per-row keys to
+// partials[block * stride + j].  The last block to take a ticket reduces all blocks' keys, writes the
+// tokens and re-arms the ticket, so the kernel is replay-safe with no memset.
+template <int STRIDE>
+__device__ __forceinline__ void ticket_and_finish(const unsigned long long* partials, int64_t m,
+                                                  ArgmaxScratch* scratch, int64_t* tokens) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    __shared__ bool last;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __threadfence();
+        const unsigned int ticket = atomicAdd(&scratch->done, 1u);
+        last = ticket == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    __shared__ unsigned long long fin[kWaves][STRIDE];
+    for (int j = 0; j < STRIDE && j < m; ++j) {
+        unsigned long long b = 0ull;
+        for (int64_t q = threadIdx.x; q < gridDim.x; q += kThreads) {
+            const unsigned long long p = __hip_atomic_load(&partials[q * STRIDE + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            b = p > b ? p : b;
+        }
+        b = wave_max(b);
+        if (lane == 0) fin[wave][j] = b;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int j = 0; j < STRIDE && j < m; ++j) {
+            unsigned long long b = fin[0][j];
+            for (int q = 1; q < kWaves; ++q) b = fin[q][j] > b ? fin[q][j] : b;
+            tokens[j] = key_index(b);
+        }
+        scratch->done = 0u;  // re-arm for the next call / graph replay
+    }
+}
 
 // Transposing butterfly over the wave: v[0..V) holds V partial sums per lane (V a power of two
 // <= 64).  Each exchange step halves the values a lane keeps (the lane keeps the half selected by
@@ -226,42 +268,129 @@ __global__ __launch_bounds__(kThreads) void gemv_argmax_kernel(const uint8_t* __
     __shared__ unsigned long long red[kWaves * 64];
     red[threadIdx.x] = best;
     __syncthreads();
-    __shared__ bool last;
     if (threadIdx.x < MT) {
         unsigned long long b = 0ull;
         for (int q = 0; q < kWaves * 64; ++q)
             if (((q & 63) >> kShift) % MT == (int)threadIdx.x) b = red[q] > b ? red[q] : b;
         partials[(int64_t)blockIdx.x * MT + threadIdx.x] = b;
     }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __threadfence();
-        const unsigned int ticket = atomicAdd(&scratch->done, 1u);
-        last = ticket == gridDim.x - 1;
+    ticket_and_finish<MT>(partials, m, scratch, tokens);
+}
+
+// ---- m >= 2: MFMA kernel --------------------------------------------------------------------------
+// A block walks vocabulary tiles of 16 rows (grid-stride).  Its 4 waves split K: wave w owns the
+// SPW consecutive steps starting at w*SPW, a step being 32 BF16 (v_mfma_f32_16x16x32_bf16) or 128 FP8
+// (v_mfma_scale_f32_16x16x128_f8f6f4, unit scales) values of K.  The activation rows are the A operand
+// and stay in registers for the whole kernel; each tile's weight rows are the B operand, loaded
+// straight from HBM, and the next tile's loads are issued before the current tile is reduced.  Lane
+// l supplies row l%16 (activation row / vocabulary row) and the l/16-th 16-byte (BF16) or 32-byte
+// (FP8) slice of the step, for A and B alike.  The four partial 16x16 tiles meet in LDS (double
+// buffered: one barrier per tile) and thread t finishes activation row t/16 of vocabulary row t%16.
+template <int KIND, int SPW>
+__global__ __launch_bounds__(kThreads) void gemv_argmax_mfma_kernel(const uint8_t* __restrict__ a, int64_t m,
+                                                                    int64_t k, const uint8_t* __restrict__ w,
+                                                                    int64_t v, HeadParams hp,
+                                                                    unsigned long long* __restrict__ partials,
+                                                                    ArgmaxScratch* __restrict__ scratch,
+                                                                    int64_t* __restrict__ tokens) {
+    constexpr int esize = KIND == 0 ? 2 : 1;
+    constexpr int SB = KIND == 0 ? 16 : 32;  // bytes per lane per step
+    constexpr int NV = SB / 16;              // 16-byte loads per lane per step
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int fr = lane & 15;
+    const int64_t row_bytes = k * esize;
+    // this lane's byte offsets in a row, one per step; slices past the row read byte 0 and are zeroed
+    int64_t off[SPW];
+    bool live[SPW];
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) {
+        const int64_t o = (int64_t)(wave * SPW + s) * (4 * SB) + (lane >> 4) * SB;
+        live[s] = o < row_bytes;
+        off[s] = live[s] ? o : 0;
     }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    // Last block: reduce the partials of every block.
-    __shared__ unsigned long long fin[kWaves][MT];
-    for (int j = 0; j < MT; ++j) {
-        unsigned long long b = 0ull;
-        for (int64_t q = threadIdx.x; q < gridDim.x; q += kThreads) {
-            const unsigned long long p = __hip_atomic_load(&partials[q * MT + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            b = p > b ? p : b;
+    uint4 xa[SPW][NV];
+    {
+        const bool arow = fr < m;
+        const uint8_t* ar = a + (arow ? fr : 0) * row_bytes;
+#pragma unroll
+        for (int s = 0; s < SPW; ++s)
+#pragma unroll
+            for (int q = 0; q < NV; ++q) {
+                const uint4 x = *reinterpret_cast<const uint4*>(ar + off[s] + 16 * q);
+                xa[s][q] = (arow && live[s]) ? x : make_uint4(0, 0, 0, 0);
+            }
+    }
+    const int64_t ntiles = (v + 15) / 16;
+    uint4 wv[SPW][NV], wn[SPW][NV];
+    auto load_tile = [&](int64_t tile, uint4 (&dst)[SPW][NV]) {
+        int64_t row = tile * 16 + fr;
+        row = row < v ? row : v - 1;
+        const uint8_t* wr = w + row * row_bytes;
+#pragma unroll
+        for (int s = 0; s < SPW; ++s)
+#pragma unroll
+            for (int q = 0; q < NV; ++q) dst[s][q] = load_stream16(wr + off[s] + 16 * q);
+    };
+    __shared__ float red[2][kWaves][16][17];
+    const int my_m = threadIdx.x >> 4, my_c = threadIdx.x & 15;
+    unsigned long long best = 0ull;
+    int buf = 0;
+    int64_t tile = blockIdx.x;
+    if (tile < ntiles) load_tile(tile, wv);
+    for (; tile < ntiles; tile += gridDim.x) {
+        if (tile + gridDim.x < ntiles) load_tile(tile + gridDim.x, wn);
+        v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < SPW; ++s) {
+            uint4 b0 = wv[s][0];
+            if (!live[s]) b0 = make_uint4(0, 0, 0, 0);
+            if constexpr (KIND == 0) {
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xa[s][0]), __builtin_bit_cast(v8bf, b0),
+                                                              acc, 0, 0, 0);
+            } else {
+                uint4 b1 = wv[s][NV - 1];
+                if (!live[s]) b1 = make_uint4(0, 0, 0, 0);
+                const v8i av = v8i{(int)xa[s][0].x, (int)xa[s][0].y, (int)xa[s][0].z, (int)xa[s][0].w,
+                                   (int)xa[s][NV - 1].x, (int)xa[s][NV - 1].y, (int)xa[s][NV - 1].z, (int)xa[s][NV - 1].w};
+                const v8i bv = v8i{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+                acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc, KIND == 2 ? 1 : 0, KIND == 2 ? 1 : 0,
+                                                                      0, 127, 0, 127);
+            }
         }
-        b = wave_max(b);
-        if (lane == 0) fin[wave][j] = b;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int j = 0; j < MT && j < m; ++j) {
-            unsigned long long b = fin[0][j];
-            for (int q = 1; q < kWaves; ++q) b = fin[q][j] > b ? fin[q][j] : b;
-            tokens[j] = key_index(b);
+        // C fragment of lane l: vocabulary row l%16 of the tile, activation rows 4*(l/16) .. +3.
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[buf][wave][(lane >> 4) * 4 + r][fr] = acc[r];
+        __syncthreads();
+        float sum = red[buf][0][my_m][my_c] + red[buf][1][my_m][my_c] + red[buf][2][my_m][my_c] + red[buf][3][my_m][my_c];
+        const int64_t row = tile * 16 + my_c;
+        if (my_m < m && row < v) {
+            uint16_t bf;
+            if constexpr (KIND == 0) {
+                bf = fhip::bf16_encode(sum);
+            } else {
+                const uint8_t code = fhip::fp8_encode(sum * hp.ab_scale / hp.out_scale, KIND == 2);
+                sum = fhip::fp8_decode(code, KIND == 2) * hp.out_scale;
+                bf = fhip::bf16_encode(sum);
+            }
+            const unsigned long long key = make_key(bf, row);
+            best = key > best ? key : best;
+            if (hp.logits != nullptr) hp.logits[my_m * v + row] = sum;
         }
-        scratch->done = 0u;  // re-arm for the next call / graph replay
+        buf ^= 1;
+#pragma unroll
+        for (int s = 0; s < SPW; ++s)
+#pragma unroll
+            for (int q = 0; q < NV; ++q) wv[s][q] = wn[s][q];
     }
+    // 16 consecutive threads share an activation row: reduce within the group, one key per row.
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) {
+        const unsigned long long x = __shfl_xor(best, o, 64);
+        best = x > best ? x : best;
+    }
+    if (my_c == 0) partials[(int64_t)blockIdx.x * 16 + my_m] = best;
+    ticket_and_finish<16>(partials, m, scratch, tokens);
 }
 
 template <int KIND>
@@ -281,6 +410,25 @@ int launch(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k, const uint8
     if (rc != FHIP_OK) return rc;
     auto* partials = static_cast<unsigned long long*>(ws);
     const int64_t bytes = k * (KIND == 0 ? 2 : 1);
+    if (m >= 2) {
+        const int64_t step_bytes = KIND == 0 ? 64 : 128;
+        const int64_t spw_need = ((bytes + step_bytes - 1) / step_bytes + kWaves - 1) / kWaves;
+        int64_t mgrid = (v + 15) / 16;
+        if (mgrid > cap) mgrid = cap;
+#define FHIP_ARGMAX_MFMA_CASE(SPW)                                                                                  \
+        if (spw_need <= SPW) {                                                                                      \
+            gemv_argmax_mfma_kernel<KIND, SPW><<<(unsigned)mgrid, kThreads, 0, ctx->stream>>>(a, m, k, w, v, hp,    \
+                                                                                   partials, ctx->scratch, tokens); \
+            ctx->last_backend = name;                                                                               \
+            FHIP_CHECK_LAUNCH(ctx, "gemv_argmax_mfma_kernel");                                                      \
+            return FHIP_OK;                                                                                         \
+        }
+        FHIP_ARGMAX_MFMA_CASE(2)
+        FHIP_ARGMAX_MFMA_CASE(4)
+        FHIP_ARGMAX_MFMA_CASE(8)
+        FHIP_ARGMAX_MFMA_CASE(KIND == 0 ? 16 : 8)
+#undef FHIP_ARGMAX_MFMA_CASE
+    }
     const int t = bytes <= 1024 ? 1 : (bytes <= 2048 ? 2 : 4);
 #define FHIP_ARGMAX_CASE(MT, T)                                                                                   \
     if (m <= MT && t == T) {                                                                                      \
@@ -293,12 +441,6 @@ int launch(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k, const uint8
     FHIP_ARGMAX_CASE(1, 1)
     FHIP_ARGMAX_CASE(1, 2)
     FHIP_ARGMAX_CASE(1, 4)
-    FHIP_ARGMAX_CASE(8, 1)
-    FHIP_ARGMAX_CASE(8, 2)
-    FHIP_ARGMAX_CASE(8, 4)
-    FHIP_ARGMAX_CASE(16, 1)
-    FHIP_ARGMAX_CASE(16, 2)
-    FHIP_ARGMAX_CASE(16, 4)
 #undef FHIP_ARGMAX_CASE
     return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "gemv_argmax: m > 16");
 }

@@ -64,31 +64,52 @@ def test_bf16_argmax_config5(ctx, m):
         assert np.max(np.abs(lg - ref)) <= 1e-2 * np.max(np.abs(ref))
 
 
-def test_bf16_argmax_special_values(ctx):
+@pytest.mark.parametrize("m", [1, 3])
+def test_bf16_argmax_special_values(ctx, m):
     """NaN rows skipped, ties and +0/-0 keep the lowest index, all-NaN gives 0
-    (test/qwen_gemm_argmax_test.cc:231-251)."""
+    (test/qwen_gemm_argmax_test.cc:231-251).  m = 3 repeats the activation row on the MFMA kernel:
+    K = 64 leaves three of its four waves with no K slice, V = 300 ends in a partial tile."""
     k = 64
-    a = po.bf16_encode(np.ones((1, k), np.float32))
+    a = po.bf16_encode(np.ones((m, k), np.float32))
     v = 300
     w = np.zeros((v, k), np.uint16)
     w[5] = po.bf16_encode(np.full(k, np.nan, np.float32))
     w[7] = 0x8000  # -0 rows give -0 sums: equal to +0
-    tokens = torch.empty(1, dtype=torch.int64, device="cuda")
-    ctx.bf16_gemv_argmax(dev(a), dev(w), tokens)
-    assert tokens.item() == po.bf16_gemm_argmax(a[0], w) == 0
+    tokens = torch.empty(m, dtype=torch.int64, device="cuda")
+
+    def run(wt, expect):
+        ctx.bf16_gemv_argmax(dev(a), dev(wt), tokens)
+        assert po.bf16_gemm_argmax(a[0], wt) == expect
+        assert tokens.cpu().numpy().tolist() == [expect] * m
+    run(w, 0)
     w[250] = po.bf16_encode(np.full(k, 0.5, np.float32))
     w[260] = w[250]
-    ctx.bf16_gemv_argmax(dev(a), dev(w), tokens)
-    assert tokens.item() == po.bf16_gemm_argmax(a[0], w) == 250
-    wn = np.tile(w[5], (v, 1))
-    ctx.bf16_gemv_argmax(dev(a), dev(wn), tokens)
-    assert tokens.item() == po.bf16_gemm_argmax(a[0], wn) == 0
+    run(w, 250)
+    w[299] = po.bf16_encode(np.full(k, 0.75, np.float32))  # the last row, in the partial tile
+    run(w, 299)
+    run(np.tile(w[5], (v, 1)), 0)
     # negative values only: the largest (closest to zero) wins, first among equals
     wneg = po.bf16_encode(-np.abs(rng(3).standard_normal((v, k))).astype(np.float32))
     wneg[123] = po.bf16_encode(np.full(k, -1e-3, np.float32))
     wneg[124] = wneg[123]
-    ctx.bf16_gemv_argmax(dev(a), dev(wneg), tokens)
-    assert tokens.item() == po.bf16_gemm_argmax(a[0], wneg) == 123
+    run(wneg, 123)
+
+
+@pytest.mark.parametrize("m,k", [(2, 2048), (16, 1024), (5, 136)])
+def test_bf16_argmax_mfma_shapes(ctx, m, k):
+    """The MFMA kernel over its K splits (K = 2048: 16 steps per wave; K = 136: a partial last slice)
+    and row counts up to 16, with the logits output."""
+    v = 20011
+    a, w = head_inputs(SEEDS[5] + 7 * m + k, m, k, v)
+    tokens = torch.empty(m, dtype=torch.int64, device="cuda")
+    logits = torch.empty((m, v), dtype=torch.float32, device="cuda")
+    ctx.bf16_gemv_argmax(dev(a), dev(w), tokens, logits)
+    flips = check_tokens(a, w, tokens.cpu().numpy())
+    assert flips <= max(1, m // 4)
+    lg = logits.cpu().numpy()
+    for j in range(m):
+        _, ref = po.bf16_gemm_argmax(a[j], w, want_logits=True)
+        assert np.max(np.abs(lg[j] - ref)) <= 1e-2 * np.max(np.abs(ref))
 
 
 def test_bf16_argmax_repeated_calls_rearm(ctx):
@@ -102,20 +123,23 @@ def test_bf16_argmax_repeated_calls_rearm(ctx):
 
 
 @pytest.mark.parametrize("dtype", [po.FP8E4M3, po.FP8E5M2])
-def test_fp8_argmax_head(ctx, dtype):
+@pytest.mark.parametrize("m,k", [(1, 1024), (5, 1024), (3, 4096)])
+def test_fp8_argmax_head(ctx, dtype, m, k):
     from tests.common import fp8_tensor, fp8_pow2_scale
-    k, v = 1024, 32768
-    r = rng(SEEDS[5])
-    a_codes, sa = fp8_tensor(r.standard_normal((1, k)).astype(np.float32), dtype)
+    v = 32768
+    r = rng(SEEDS[5] + m)
+    a_codes, sa = fp8_tensor(r.standard_normal((m, k)).astype(np.float32), dtype)
     w_codes, sw = fp8_tensor(r.standard_normal((v, k), dtype=np.float32) * np.float32(0.02), dtype)
     sums = po.fp8_sums(dtype, a_codes, sa, w_codes, sw, True)
     s_out = fp8_pow2_scale(float(np.abs(sums).max()), dtype)
-    tokens = torch.empty(1, dtype=torch.int64, device="cuda")
+    tokens = torch.empty(m, dtype=torch.int64, device="cuda")
     ctx.fp8_gemv_argmax(dtype, dev(a_codes), sa, dev(w_codes), sw, s_out, tokens)
-    ref = po.fp8_gemm_argmax(dtype, a_codes, sa, w_codes, sw, s_out)
-    got = tokens.item()
-    if got != ref:
-        # FP8 output quantization creates many ties; accept only an equal-valued earlier/later candidate
-        # whose sums straddle an FP8 code boundary by accumulation-order rounding.
-        vals = po.cast_from_fp8(dtype, po.fp8_gemm(dtype, a_codes, sa, w_codes, sw, True, s_out), s_out, po.FP32)[0]
-        assert abs(vals[got] - vals[ref]) <= abs(vals[ref]) * 0.13, (got, ref)
+    vals_all = po.cast_from_fp8(dtype, po.fp8_gemm(dtype, a_codes, sa, w_codes, sw, True, s_out), s_out, po.FP32)
+    for j in range(m):
+        ref = po.fp8_gemm_argmax(dtype, a_codes[j], sa, w_codes, sw, s_out)
+        got = int(tokens[j].item())
+        if got != ref:
+            # FP8 output quantization creates many ties; accept only an equal-valued earlier/later candidate
+            # whose sums straddle an FP8 code boundary by accumulation-order rounding.
+            vals = vals_all[j]
+            assert abs(vals[got] - vals[ref]) <= abs(vals[ref]) * 0.13, (j, got, ref)
