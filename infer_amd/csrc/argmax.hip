@@ -96,9 +96,19 @@ struct HeadParams {
     float* logits;    // optional [m][v]
 };
 
-// Publishes nothing itself: called by every block after it wrote its per-row keys to
-// partials[block * stride + j].  The last block to take a ticket reduces all blocks' keys, writes the
-// tokens and re-arms the ticket, so the kernel is replay-safe with no memset.
+// Cross-block hand-off without cache-wide fences.  The L2 is per XCD and not coherent between XCDs,
+// so an agent-scope fence writes back and invalidates the whole L2 of the block's XCD -- tens of
+// nanoseconds per block, serialized.  The only data handed over are the per-block keys, so they move
+// with agent-scope atomic stores (written through to the coherent level) and are read back with
+// agent-scope atomic loads; `s_waitcnt vmcnt(0)` makes every key store complete before the block
+// takes its ticket, and the ticket atomics are device-coherent.
+__device__ __forceinline__ void publish_key(unsigned long long* slot, unsigned long long key) {
+    __hip_atomic_store(slot, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Called by every block after it published its per-row keys to partials[block * stride + j].  The
+// last block to take a ticket reduces all blocks' keys, writes the tokens and re-arms the tickets,
+// so the kernel is replay-safe with no memset.
 template <int STRIDE>
 __device__ __forceinline__ void ticket_and_finish(const unsigned long long* partials, int64_t m,
                                                   ArgmaxScratch* scratch, int64_t* tokens) {
@@ -107,13 +117,24 @@ __device__ __forceinline__ void ticket_and_finish(const unsigned long long* part
     __shared__ bool last;
     __syncthreads();
     if (threadIdx.x == 0) {
-        __threadfence();
-        const unsigned int ticket = atomicAdd(&scratch->done, 1u);
-        last = ticket == gridDim.x - 1;
+        // block b counts in group b % G; the group's last block counts in `done`
+        const unsigned int groups = gridDim.x < (unsigned)kTicketGroups ? gridDim.x : (unsigned)kTicketGroups;
+        const unsigned int g = blockIdx.x % groups;
+        const unsigned int members = (gridDim.x - g + groups - 1) / groups;
+        __builtin_amdgcn_s_waitcnt(0);  // this block's key stores (threads < 16, same wave) are complete
+        bool top = false;
+        const unsigned int t = __hip_atomic_fetch_add(&scratch->group_done[g][0], 1u, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+        if (t == members - 1) {
+            // every member has counted: re-arm the group
+            __hip_atomic_store(&scratch->group_done[g][0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            top = __hip_atomic_fetch_add(&scratch->done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                  groups - 1;
+        }
+        last = top;
     }
     __syncthreads();
     if (!last) return;
-    __threadfence();
     __shared__ unsigned long long fin[kWaves][STRIDE];
     for (int j = 0; j < STRIDE && j < m; ++j) {
         unsigned long long b = 0ull;
@@ -131,7 +152,7 @@ __device__ __forceinline__ void ticket_and_finish(const unsigned long long* part
             for (int q = 1; q < kWaves; ++q) b = fin[q][j] > b ? fin[q][j] : b;
             tokens[j] = key_index(b);
         }
-        scratch->done = 0u;  // re-arm for the next call / graph replay
+        __hip_atomic_store(&scratch->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // re-arm
     }
 }
 
@@ -272,7 +293,7 @@ __global__ __launch_bounds__(kThreads) void gemv_argmax_kernel(const uint8_t* __
         unsigned long long b = 0ull;
         for (int q = 0; q < kWaves * 64; ++q)
             if (((q & 63) >> kShift) % MT == (int)threadIdx.x) b = red[q] > b ? red[q] : b;
-        partials[(int64_t)blockIdx.x * MT + threadIdx.x] = b;
+        publish_key(&partials[(int64_t)blockIdx.x * MT + threadIdx.x], b);
     }
     ticket_and_finish<MT>(partials, m, scratch, tokens);
 }
@@ -389,7 +410,11 @@ __global__ __launch_bounds__(kThreads) void gemv_argmax_mfma_kernel(const uint8_
         const unsigned long long x = __shfl_xor(best, o, 64);
         best = x > best ? x : best;
     }
-    if (my_c == 0) partials[(int64_t)blockIdx.x * 16 + my_m] = best;
+    // keys leave through wave 0 (threads 0..15), whose own wait covers them before the ticket
+    __shared__ unsigned long long row_key[16];
+    if (my_c == 0) row_key[my_m] = best;
+    __syncthreads();
+    if (threadIdx.x < 16) publish_key(&partials[(int64_t)blockIdx.x * 16 + threadIdx.x], row_key[threadIdx.x]);
     ticket_and_finish<16>(partials, m, scratch, tokens);
 }
 

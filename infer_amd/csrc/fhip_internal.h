@@ -11,13 +11,16 @@
 
 #include "../../include/fhip.h"
 
-// Persistent per-context device scratch: argmax candidate keys and the block-completion counter.
-// Every kernel that uses it leaves it zeroed on exit, so calls and graph replays need no memset.
+// Persistent per-context device scratch: the argmax block-completion counters, two levels (blocks
+// count in per-group counters, the last block of each group counts in `done`) so that no single
+// address takes an atomic from every block.  Each counter has its own 128-byte line.  Every kernel
+// that uses them leaves them zeroed on exit, so calls and graph replays need no memset.
 constexpr int kArgmaxMaxRows = 16;
+constexpr int kTicketGroups = 32;
 struct ArgmaxScratch {
-    unsigned long long keys[kArgmaxMaxRows];
     unsigned int done;
     unsigned int pad[31];
+    unsigned int group_done[kTicketGroups][32];  // [g][0] is the counter
 };
 
 struct fhip_weight_s;
