@@ -9,8 +9,11 @@ weight from HBM.  Steps are captured once into a HIP graph through the library's
 (fhip_capture_*) and the graph is replayed; the timed region is bracketed by a device
 synchronisation on both sides.
 
-`roofline`: the dominant kernel's algorithmic bytes / its average duration from HIP event pairs
-around every launch, recorded on the kernel's stream during a separate eager pass.
+`roofline`: the headline kernel's algorithmic bytes / its average launch duration.  Each timed step is
+exactly one launch of that kernel, so the average duration is the timed region (HIP events on the
+kernel's stream) over the launch count; per-launch event pairs from a separate eager pass are reported
+beside it (they include the event overhead).  `traffic` is the HBM bytes per launch measured by
+rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated on a copy kernel (profiles/fp8_gemv_decode_m1.*).
 `cpu_baseline`: the reference's own x86 FP8 linear (oracle/_ref, built from the Feather sources)
 on the host, M=1 with its prepared (BF16-packed) weight, for a bounded ~10 s sample.
 `configs`: the other BASELINE.json configs (C1, C2 M=4/16, C3, C4, C5), same method.
@@ -30,6 +33,8 @@ HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
 INT8_PEAK_TOPS = 5000.0
 METRIC = "FP8/INT8 GEMM TOPS (% MFMA peak) + decode GEMV HBM GB/s (% peak), 1 GPU"
+# library backend name of the headline call -> the kernel it launches (as rocprofv3 names it)
+HEADLINE_KERNELS = {"fp8_gemv_m1": "fp8_gemv1_kernel<false, 1, 2, 2>"}
 
 
 def parse():
@@ -155,7 +160,7 @@ def headline(b, args):
     res = {
         "ms_per_step": ms, "steps": reps * per_graph, "wall_s": wall, "bytes": bytes_step,
         "value": bytes_step / (ms * 1e-3) / 1e9, "kernel_ms": kmean, "kernel_ms_median": kmed,
-        "backend": backend,
+        "backend": backend, "backend_kernel": HEADLINE_KERNELS.get(backend),
     }
     for wt in weights:
         wt.release()
@@ -318,6 +323,18 @@ def extra_configs(b, args):
     return res
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (profiles/fp8_gemv_decode_m1.traffic.json), or None when that summary is of another kernel."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "fp8_gemv_decode_m1.traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    return t["bytes_per_launch"] if t.get("kernel") == kernel else None
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -344,10 +361,13 @@ def main():
                         "Cast(bf16) fused in one kernel; 80 rotated weight copies (294 MB)",
             "kernel": h["backend"], "graph_replayed": True,
         },
+        # Each timed step is exactly one launch of the headline kernel, so the kernel's average launch
+        # duration is the timed region over the launch count (events on the kernel's stream).
         "roofline": {
-            "bound": "hbm", "achieved": round(h["bytes"] / h["kernel_ms"] / 1e6, 2), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(h["bytes"] / h["kernel_ms"] / 1e6 / HBM_PEAK_GBS, 4),
-            "traffic": None, "kernel_ms": h["kernel_ms"], "kernel_ms_median": h["kernel_ms_median"],
+            "bound": "hbm", "achieved": round(h["bytes"] / h["ms_per_step"] / 1e6, 2), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(h["bytes"] / h["ms_per_step"] / 1e6 / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic(h["backend_kernel"]), "kernel_ms": h["ms_per_step"],
+            "kernel_ms_event_pairs": h["kernel_ms"], "kernel_ms_event_pairs_median": h["kernel_ms_median"],
         },
         "cpu_baseline": None,
     }
