@@ -12,8 +12,8 @@
 //     pitch: the 16 lanes of a ds_read_b128 group hit 16 distinct 4-bank groups (5*r mod 16 distinct);
 //   * two LDS stages: the global loads of stage s+1 are in flight while stage s feeds the MFMAs;
 //   * tile order is XCD-aware: consecutive workgroups land on different XCDs (round-robin dispatch),
-//     so the tile index is re-derived to give each XCD a contiguous block of tiles (shared operand rows
-//     stay in that XCD's L2);
+//     so the tile index is re-derived to give each XCD a rectangle of tiles whose shared operand rows
+//     fit in that XCD's L2 (XcdMap);
 //   * epilogue: accumulators -> output bits -> LDS tile -> coalesced 16-byte global stores.
 #include "fp8_common.h"
 
@@ -23,8 +23,6 @@ namespace {
 
 using namespace fhip;
 
-constexpr int kBK = 64;
-constexpr int kStages = 4;
 
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [0, N).  Used where the accumulator
 // registers are indexed, so no index is ever a runtime value (which would demote them to scratch).
@@ -37,23 +35,26 @@ __device__ __forceinline__ void static_for(F&& f) {
     static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// LDS stage: A rows [BM][64 B], then B rows [BNP][64 B] (BNP = BN rounded up to 64 rows so every
-// wave issues the same number of 16-byte loads).  Rows are unpadded; the 16-byte chunk c of row r
-// sits at position c ^ swz(r), swz(r) = (r >> 2) & 3, which keeps the 16 lanes of every
-// ds_read_b128 group on 16 distinct 4-bank groups.
-template <int BM, int BN, int NT>
+// LDS stage: A rows [BM][BK bytes], then B rows [BNP][BK] (BNP = BN rounded up so every wave issues
+// the same number of 16-byte loads).  Rows are unpadded; the 16-byte chunk c of row r sits at position
+// c ^ swz(r): BK = 64 (4 chunks): swz(r) = (r >> 2) & 3; BK = 128 (8 chunks): swz(r) = (r >> 1) & 7.  Both
+// keep the 16 lanes of every ds_read_b128 group (16 consecutive rows, one chunk) on 16 distinct 16-byte
+// bank groups.
+template <int BM, int BN, int NT, int BK>
 struct Stage {
-    static constexpr int kRowsPerPass = NT / 4;    // one pass of 16-byte loads covers NT/4 rows
+    static constexpr int kChunks = BK / 16;             // 16-byte chunks per row
+    static constexpr int kRowsPerPass = NT / kChunks;   // one pass of 16-byte loads covers these rows
     static constexpr int BNP = (BN + kRowsPerPass - 1) / kRowsPerPass * kRowsPerPass;
-    static constexpr int kA = BM * kBK;
-    static constexpr int kBytes = (BM + BNP) * kBK;
-    static constexpr int kLoadsA = BM * 4 / NT;    // 16-byte loads per thread per stage
-    static constexpr int kLoadsB = BNP * 4 / NT;
+    static constexpr int kA = BM * BK;
+    static constexpr int kBytes = (BM + BNP) * BK;
+    static constexpr int kLoadsA = BM * kChunks / NT;   // 16-byte loads per thread per stage
+    static constexpr int kLoadsB = BNP * kChunks / NT;
     static constexpr int kLoads = kLoadsA + kLoadsB;
-    static_assert(kLoadsA * NT == BM * 4, "BM must be a multiple of NT/4");
+    static_assert(kLoadsA * NT == BM * kChunks, "BM must be a multiple of NT/kChunks");
 };
 
-__device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
+template <int BK>
+__device__ __forceinline__ int swz(int r) { return BK == 64 ? (r >> 2) & 3 : (r >> 1) & 7; }
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
@@ -138,12 +139,21 @@ __device__ __forceinline__ void fast_value4(const Fp8Epilogue& ep, float mul, co
     }
 }
 
-template <bool E5, int BM, int BN, int WAVES_M, int WAVES_N, int OUT_BYTES, bool POW2>
+// Tile -> XCD assignment.  Workgroups are dispatched round-robin over the 8 XCDs, each with its own
+// L2.  When the tile grid splits into 8 equal rectangles (gm x gn rectangles of rm x rn tiles), XCD x
+// takes rectangle x, chosen so that the A rows and B columns its tiles share (rm*BM + rn*BN rows of
+// K bytes) are as few as possible; otherwise consecutive tile indices go to the same XCD.
+struct XcdMap {
+    int gn, rm, rn;  // rm == 0: no rectangle split
+};
+
+template <bool E5, int BM, int BN, int WAVES_M, int WAVES_N, int OUT_BYTES, bool POW2, int BK, int STAGES>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const uint8_t* __restrict__ a, int64_t m, int64_t k,
                                                        const uint8_t* __restrict__ b, int64_t kp, int64_t np,
-                                                       int tiles_n, int tiles_total, Fp8Epilogue ep) {
+                                                       int tiles_n, int tiles_total, XcdMap xm, Fp8Epilogue ep) {
     constexpr int NT = 64 * WAVES_M * WAVES_N;
-    using S = Stage<BM, BN, NT>;
+    using S = Stage<BM, BN, NT, BK>;
+    constexpr int kSub = BK / 64;  // 64-deep MFMA steps per stage
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int FM = WTM / 32, FN = WTN / 32;
     static_assert(FM * 32 == WTM && FN * 32 == WTN, "wave tile must be a multiple of 32");
@@ -156,8 +166,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
     int tile = blockIdx.x;
-    const int nb = gridDim.x;
-    if ((nb & 7) == 0) tile = (tile & 7) * (nb >> 3) + (tile >> 3);
+    if (xm.rm > 0) {
+        // workgroup b runs on XCD b % 8; XCD x takes the x-th rm x rn rectangle of tiles
+        const int x = tile & 7, l = tile >> 3;
+        tile = ((x / xm.gn) * xm.rm + l / xm.rn) * tiles_n + (x % xm.gn) * xm.rn + l % xm.rn;
+    } else if ((gridDim.x & 7) == 0) {
+        tile = (tile & 7) * (gridDim.x >> 3) + (tile >> 3);
+    }
     if (tile >= tiles_total) return;
     const int64_t m0 = (int64_t)(tile / tiles_n) * BM;
     const int64_t n0 = (int64_t)(tile % tiles_n) * BN;
@@ -168,8 +183,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
     for (int i = 0; i < S::kLoads; ++i) {
         const bool is_a = i < S::kLoadsA;
         const int q = (is_a ? i : i - S::kLoadsA) * NT + tid;
-        const int r = q >> 2;
-        const int c = (q & 3) ^ swz(r);
+        const int r = q / S::kChunks;
+        const int c = (q % S::kChunks) ^ swz<BK>(r);
         if (is_a) {
             const int64_t row = m0 + r < m ? m0 + r : m - 1;   // rows past m are computed, never stored
             src[i] = a + row * k + c * 16;
@@ -179,13 +194,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
         }
     }
     auto issue = [&](int kt) {
-        uint8_t* st = smem + (kt % kStages) * S::kBytes;
+        uint8_t* st = smem + (kt % STAGES) * S::kBytes;
 #pragma unroll
         for (int i = 0; i < S::kLoads; ++i) {
             const bool is_a = i < S::kLoadsA;
             const int slot = is_a ? i : i - S::kLoadsA;
             uint8_t* dst = st + (is_a ? 0 : S::kA) + (slot * NT + wave * 64) * 16;
-            load_to_lds(src[i] + (int64_t)kt * kBK, dst);
+            load_to_lds(src[i] + (int64_t)kt * BK, dst);
         }
     };
 
@@ -197,53 +212,62 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    const int nk = (int)(k / kBK);  // host guarantees k % 64 == 0
+    const int nk = (int)(k / BK);  // host guarantees k % BK == 0
 #pragma unroll
-    for (int s0 = 0; s0 < kStages - 1; ++s0)
+    for (int s0 = 0; s0 < STAGES - 1; ++s0)
         if (s0 < nk) issue(s0);
 
     const int frag_row = lane & 31;
     const int frag_c = (lane >> 5) * 2;
     for (int kt = 0; kt < nk; ++kt) {
-        const int ahead = nk - 1 - kt;  // stages issued after kt (capped below)
-        if (ahead >= 2) wait_vmcnt<2 * S::kLoads>();
-        else if (ahead == 1) wait_vmcnt<S::kLoads>();
+        // stages issued after kt: min(STAGES - 2, nk - 1 - kt); wait until at most that many are in flight
+        const int ahead = nk - 1 - kt;
+        if (STAGES >= 4 && ahead >= 2) wait_vmcnt<2 * S::kLoads>();
+        else if (STAGES >= 3 && ahead >= 1) wait_vmcnt<S::kLoads>();
         else wait_vmcnt<0>();
         // Plain s_barrier: the explicit vmcnt wait above already covers this wave's stage loads, and a
         // __syncthreads() fence would also wait for the loads of the stages still in flight.
         __builtin_amdgcn_s_barrier();
-        if (kt + kStages - 1 < nk) issue(kt + kStages - 1);
-        const uint8_t* sa = smem + (kt % kStages) * S::kBytes;
+        if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1);
+        const uint8_t* sa = smem + (kt % STAGES) * S::kBytes;
         const uint8_t* sb = sa + S::kA;
-        u32x4_t fa[FM][2], fb[FN][2];
+        u32x4_t fa[kSub][FM][2], fb[kSub][FN][2];
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            const int r = wm * WTM + i * 32 + frag_row;
-            const uint8_t* row = sa + r * kBK;
-            fa[i][0] = lds_read16(row + ((frag_c ^ swz(r)) << 4));
-            fa[i][1] = lds_read16(row + (((frag_c + 1) ^ swz(r)) << 4));
-        }
+        for (int u = 0; u < kSub; ++u) {
+            const int c0 = u * 4 + frag_c;
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int r = wn * WTN + j * 32 + frag_row;
-            const uint8_t* row = sb + r * kBK;
-            fb[j][0] = lds_read16(row + ((frag_c ^ swz(r)) << 4));
-            fb[j][1] = lds_read16(row + (((frag_c + 1) ^ swz(r)) << 4));
+            for (int i = 0; i < FM; ++i) {
+                const int r = wm * WTM + i * 32 + frag_row;
+                const uint8_t* row = sa + r * BK;
+                fa[u][i][0] = lds_read16(row + ((c0 ^ swz<BK>(r)) << 4));
+                fa[u][i][1] = lds_read16(row + (((c0 + 1) ^ swz<BK>(r)) << 4));
+            }
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int r = wn * WTN + j * 32 + frag_row;
+                const uint8_t* row = sb + r * BK;
+                fb[u][j][0] = lds_read16(row + ((c0 ^ swz<BK>(r)) << 4));
+                fb[u][j][1] = lds_read16(row + (((c0 + 1) ^ swz<BK>(r)) << 4));
+            }
         }
         // Wait for the fragment reads; every fragment register is an operand, so no MFMA that uses one
         // can be scheduled above the wait.
-        lds_fence<FM, FN>(fa, fb);
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
+        for (int u = 0; u < kSub; ++u) lds_fence<FM, FN>(fa[u], fb[u]);
 #pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                const v8i av = v8i{(int)fa[i][0].x, (int)fa[i][0].y, (int)fa[i][0].z, (int)fa[i][0].w,
-                                   (int)fa[i][1].x, (int)fa[i][1].y, (int)fa[i][1].z, (int)fa[i][1].w};
-                const v8i bv = v8i{(int)fb[j][0].x, (int)fb[j][0].y, (int)fb[j][0].z, (int)fb[j][0].w,
-                                   (int)fb[j][1].x, (int)fb[j][1].y, (int)fb[j][1].z, (int)fb[j][1].w};
-                // weight fragment as the row operand: each 32x32 block is computed transposed
-                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[i][j], fmt, fmt, 0, 127, 0, 127);
-            }
+        for (int u = 0; u < kSub; ++u)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    const v8i av = v8i{(int)fa[u][i][0].x, (int)fa[u][i][0].y, (int)fa[u][i][0].z, (int)fa[u][i][0].w,
+                                       (int)fa[u][i][1].x, (int)fa[u][i][1].y, (int)fa[u][i][1].z, (int)fa[u][i][1].w};
+                    const v8i bv = v8i{(int)fb[u][j][0].x, (int)fb[u][j][0].y, (int)fb[u][j][0].z, (int)fb[u][j][0].w,
+                                       (int)fb[u][j][1].x, (int)fb[u][j][1].y, (int)fb[u][j][1].z, (int)fb[u][j][1].w};
+                    // weight fragment as the row operand: each 32x32 block is computed transposed
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[i][j], fmt, fmt, 0, 127, 0,
+                                                                                 127);
+                }
     }
     __syncthreads();
 
@@ -296,29 +320,43 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
     }
 }
 
-template <int BM, int BN, int NT, int OUT_BYTES>
+template <int BM, int BN, int NT, int OUT_BYTES, int BK, int STAGES>
 constexpr size_t lds_bytes() {
-    constexpr size_t ops = (size_t)kStages * Stage<BM, BN, NT>::kBytes;
+    constexpr size_t ops = (size_t)STAGES * Stage<BM, BN, NT, BK>::kBytes;
     constexpr size_t epi = (size_t)BM * (BN * OUT_BYTES + 16);
     return ops > epi ? ops : epi;
 }
 
-template <bool E5, int BM, int BN, int WAVES_M, int WAVES_N>
+template <bool E5, int BM, int BN, int WAVES_M, int WAVES_N, int BK = 64, int STAGES = 4>
 int launch_tile(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, const fhip_weight_s* w,
                 const Fp8Epilogue& ep, const char* name) {
     const int64_t kp = ((w->k + 127) / 128) * 128;
     const int64_t np = ((w->n + 255) / 256) * 256;
     const int tiles_m = (int)((m + BM - 1) / BM), tiles_n = (int)((w->n + BN - 1) / BN);
     const int tiles = tiles_m * tiles_n;
-    const int grid = tiles;  // the kernel remaps tiles XCD-wise when the count divides by 8
+    const int grid = tiles;  // the kernel remaps tiles XCD-wise
+    XcdMap xm{1, 0, 1};
+    {
+        const int splits[4][2] = {{8, 1}, {4, 2}, {2, 4}, {1, 8}};
+        int64_t best = -1;
+        for (const auto& sp : splits) {
+            if (tiles_m % sp[0] != 0 || tiles_n % sp[1] != 0) continue;
+            const int rm = tiles_m / sp[0], rn = tiles_n / sp[1];
+            const int64_t rows = (int64_t)rm * BM + (int64_t)rn * BN;
+            if (best < 0 || rows < best) {
+                best = rows;
+                xm = XcdMap{sp[1], rm, rn};
+            }
+        }
+    }
     const uint8_t* wd = static_cast<const uint8_t*>(w->data);
     const bool pow2 = ep.out_inv != 0.0f;
 #define FHIP_GEMM_LAUNCH(OB, P)                                                                                     \
-    fp8_gemm_kernel<E5, BM, BN, WAVES_M, WAVES_N, OB, P><<<grid, 64 * WAVES_M * WAVES_N,                             \
-                                                          lds_bytes<BM, BN, 64 * WAVES_M * WAVES_N, OB>(), ctx->stream>>>( \
-        a, m, k64, wd, kp, np, tiles_n, tiles, ep)
+    fp8_gemm_kernel<E5, BM, BN, WAVES_M, WAVES_N, OB, P, BK, STAGES><<<grid, 64 * WAVES_M * WAVES_N,                             \
+                                                          lds_bytes<BM, BN, 64 * WAVES_M * WAVES_N, OB, BK, STAGES>(), ctx->stream>>>( \
+        a, m, k64, wd, kp, np, tiles_n, tiles, xm, ep)
     if (ep.out_dtype == FHIP_FP32) {
-        if (lds_bytes<BM, BN, 64 * WAVES_M * WAVES_N, 4>() > 160 * 1024)
+        if (lds_bytes<BM, BN, 64 * WAVES_M * WAVES_N, 4, BK, STAGES>() > 160 * 1024)
             return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "fp8 gemm: fp32 output tile too large");
         if (pow2) FHIP_GEMM_LAUNCH(4, true); else FHIP_GEMM_LAUNCH(4, false);
     } else if (ep.out_dtype == FHIP_BF16) {
@@ -335,10 +373,14 @@ int launch_tile(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, cons
 template <bool E5>
 int launch(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, const fhip_weight_s* w, const Fp8Epilogue& ep) {
     const int64_t n = w->n;
-    if (ep.out_dtype == FHIP_FP32) return launch_tile<E5, 128, 128, 2, 4>(ctx, a, m, k64, w, ep, "fp8_mfma_gemm_128x128_w8");
-    // Tile choice: fill the 256 CUs with whole tiles where the shape allows it.
-    if (((m + 255) / 256) * ((n + 255) / 256) >= 192)
-        return launch_tile<E5, 256, 256, 4, 2>(ctx, a, m, k64, w, ep, "fp8_mfma_gemm_256x256_w8");
+    // Tile choice: fill the 256 CUs with whole tiles where the shape allows it; 128-deep stages (half the
+    // barriers per MFMA) when K allows them.
+    const bool big = ((m + 255) / 256) * ((n + 255) / 256) >= 192 && ep.out_dtype != FHIP_FP32;
+    if (k64 % 128 == 0) {
+        if (big) return launch_tile<E5, 256, 256, 4, 2, 128, 2>(ctx, a, m, k64, w, ep, "fp8_mfma_gemm_256x256_bk128_w8");
+        return launch_tile<E5, 128, 128, 2, 4, 128, 4>(ctx, a, m, k64, w, ep, "fp8_mfma_gemm_128x128_bk128_w8");
+    }
+    if (big) return launch_tile<E5, 256, 256, 4, 2>(ctx, a, m, k64, w, ep, "fp8_mfma_gemm_256x256_w8");
     return launch_tile<E5, 128, 128, 2, 4>(ctx, a, m, k64, w, ep, "fp8_mfma_gemm_128x128_w8");
 }
 

@@ -134,7 +134,7 @@ def test_fp8_gemv_fused_bf16_io(ctx, dtype, m):
 
 
 @pytest.mark.parametrize("dtype", FP8)
-@pytest.mark.parametrize("shape", [(256, 1024, 512), (100, 384, 200), (4096, 1024, 3584)])
+@pytest.mark.parametrize("shape", [(256, 1024, 512), (100, 384, 200), (200, 320, 300), (4096, 1024, 3584)])
 def test_fp8_mfma_gemm_matches_oracle(ctx, dtype, shape):
     m, k, n = shape
     a, sa, w_nk, w_src, sw, s_out = _linear_case(SEEDS[3] + m, dtype, m, k, n, 1)
@@ -193,6 +193,28 @@ def test_fp8_gemv_m1_activation_encode_exact(ctx, dtype, src):
     got = host(out)
     bad = np.nonzero(got != ref)[1]
     assert bad.size == 0, f"{bad.size} mismatches: x={x[0, bad[:4]]} got={got[0, bad[:4]]} ref={ref[0, bad[:4]]}"
+    wt.release()
+
+
+@pytest.mark.parametrize("dtype", FP8)
+@pytest.mark.parametrize("out_dtype", [po.BF16, po.FP32])
+def test_fp8_gemm_decoded_outputs(ctx, dtype, out_dtype):
+    """BF16 / FP32 outputs (the FP8 code decoded with out_scale, as the exported Gemm -> Cast pair) on a
+    down-projection-like shape (K = 3584, 128-deep stages): each output must be exactly a decoded FP8 code
+    and those codes meet the FP8 tolerance."""
+    m, k, n = 300, 3584, 1024
+    a, sa, w_nk, w_src, sw, s_out = _linear_case(SEEDS[3] + 17, dtype, m, k, n, 1)
+    wt = ctx.prepare_weight(dev(w_src), dtype, k, n, 1, version=8)
+    tdt = torch.int16 if out_dtype == po.BF16 else torch.float32
+    out = torch.empty((m, n), dtype=tdt, device="cuda")
+    ctx.fp8_linear(dev(a), dtype, sa, m, wt, sw, out, out_dtype, s_out)
+    assert ctx.last_backend().startswith("fp8_mfma_gemm")
+    got = host(out, np.uint16) if out_dtype == po.BF16 else host(out)
+    codes = po.cast_to_fp8(out_dtype, got, dtype, s_out)
+    assert np.array_equal(po.cast_from_fp8(dtype, codes, s_out, out_dtype).view(got.dtype), got)
+    rows = np.sort(rng(9).choice(m, 64, replace=False))
+    ref = po.fp8_gemm(dtype, a[rows], sa, w_nk, sw, True, s_out)
+    fp8_linear_check(dtype, codes[rows], ref, a[rows], sa, w_nk, sw, s_out, f"gemm out {out_dtype}")
     wt.release()
 
 
