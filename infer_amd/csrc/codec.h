@@ -133,6 +133,35 @@ FHIP_HD uint16_t fp16_encode(float value) {
     return (uint16_t)(sign | ((uint32_t)he << 10) | (r & 0x3ffu));
 }
 
+// FP16 encode of the Cast operator (include/util/fp16.h FloatToHalf, used by src/kernel/common/cast.cc:98).
+// It differs from fp16_encode above (DequantizeLinear's encoder): the magnitude is rounded half away
+// from zero at the FP16 quantum, magnitudes below 2^-24 become a signed zero, and a NaN keeps its top
+// 10 payload bits with the lowest bit forced on.
+FHIP_HD uint16_t fp16_encode_cast(float value) {
+    const uint32_t u = f32_bits(value);
+    const uint32_t sign = (u >> 16) & 0x8000u;
+    const uint32_t fexp = (u >> 23) & 0xffu;
+    const uint32_t frac = u & 0x7fffffu;
+    if (fexp == 0xffu) return (uint16_t)(sign | 0x7c00u | (frac ? ((frac >> 13) | 1u) : 0u));
+    const int e = (int)fexp - 127;  // unbiased exponent
+    if (e > 15) return (uint16_t)(sign | 0x7c00u);
+    if (e < -24) return (uint16_t)sign;
+    if (e < -14) {
+        // subnormal result: the significand (hidden bit included) keeps its top bits, half away rounds up
+        const int drop = -e - 1;  // bits of the 24-bit significand below the FP16 quantum 2^-24
+        const uint32_t sig = frac | 0x800000u;
+        return (uint16_t)(sign | ((sig + (1u << (drop - 1))) >> drop));
+    }
+    // normal result: round the 23-bit fraction to 10 bits, half away; a carry bumps the exponent
+    uint32_t he = (uint32_t)(e + 15);
+    uint32_t f = frac + 0x1000u;
+    if (f & 0x800000u) {
+        f = 0;
+        if (++he >= 0x1fu) return (uint16_t)(sign | 0x7c00u);
+    }
+    return (uint16_t)(sign | (he << 10) | (f >> 13));
+}
+
 FHIP_HD float fp16_decode(uint16_t b) {
     const uint32_t sign = (uint32_t)(b & 0x8000u) << 16;
     const uint32_t e = (b >> 10) & 0x1fu;

@@ -357,7 +357,7 @@ __global__ void cast_kernel(const void* __restrict__ src, int src_dtype, float s
         switch (dst_dtype) {
             case FHIP_FP32: static_cast<float*>(dst)[i] = v; break;
             case FHIP_BF16: static_cast<uint16_t*>(dst)[i] = fhip::bf16_encode(v); break;
-            case FHIP_FP16: static_cast<uint16_t*>(dst)[i] = fhip::fp16_encode(v); break;
+            case FHIP_FP16: static_cast<uint16_t*>(dst)[i] = fhip::fp16_encode_cast(v); break;  // FloatToHalf
             case FHIP_FP8E4M3: static_cast<uint8_t*>(dst)[i] = fhip::fp8_encode(v / dst_scale, false); break;
             default: static_cast<uint8_t*>(dst)[i] = fhip::fp8_encode(v / dst_scale, true); break;
         }

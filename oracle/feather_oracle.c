@@ -125,6 +125,13 @@ void fo_bf16_encode_bits_range(uint32_t first_bits, int64_t count, uint16_t* out
     for (int64_t i = 0; i < count; ++i) out[i] = fo_bf16_encode(u2f(first_bits + (uint32_t)i));
 }
 
+void fo_fp16_encode_bits_range(int cast_rule, uint32_t first_bits, int64_t count, uint16_t* out) {
+    for (int64_t i = 0; i < count; ++i) {
+        float x = u2f(first_bits + (uint32_t)i);
+        out[i] = cast_rule ? fo_fp16_encode_cast(x) : fo_fp16_encode(x);
+    }
+}
+
 uint16_t fo_bf16_encode_plain(float value) {         /* quantize_linear_utils.h:110-117 */
     uint32_t u = f2u(value);
     uint32_t low = u & 0xffffu, high = u >> 16;
@@ -145,6 +152,27 @@ uint16_t fo_fp16_encode(float value) {               /* quantize_linear_utils.h:
     uint32_t r = rne_shift(frac | 0x800000u, 13);   /* 11-bit significand incl. hidden bit */
     if (r == 0x800u) return (uint16_t)(sign | ((uint32_t)(he + 1) << 10));
     return (uint16_t)(sign | ((uint32_t)he << 10) | (r & 0x3ffu));
+}
+
+/* Cast's FP16 encoder (include/util/fp16.h FloatToHalf, cast.cc:98): magnitude rounded half away
+ * from zero at the FP16 quantum, |x| < 2^-24 -> signed zero, overflow -> Inf, NaN -> top 10 payload
+ * bits with the lowest forced on.  Written as: the value is a multiple of the quantum q (2^-24 for
+ * subnormal results, 2^(e-10) for normal ones); add q/2 to the magnitude's significand and truncate. */
+uint16_t fo_fp16_encode_cast(float value) {
+    uint32_t u = f2u(value);
+    uint32_t sign = (u >> 16) & 0x8000u, fexp = (u >> 23) & 0xffu, frac = u & 0x7fffffu;
+    int e = (int)fexp - 127;
+    if (fexp == 0xffu) return (uint16_t)(sign | 0x7c00u | (frac ? ((frac >> 13) | 1u) : 0u));
+    if (e > 15) return (uint16_t)(sign | 0x7c00u);
+    if (e < -24) return (uint16_t)sign;
+    uint32_t sig = frac | 0x800000u;            /* 24-bit significand, value = sig * 2^(e-23) */
+    int drop = e < -14 ? -e - 1 : 13;           /* significand bits below the quantum */
+    uint32_t q = (sig + (1u << (drop - 1))) >> drop;   /* units of the quantum, half away */
+    if (e < -14) return (uint16_t)(sign | q);   /* subnormal (q == 0x400 is the smallest normal) */
+    /* normal: q in [0x400, 0x800]; 0x800 means the rounding carried into the next binade */
+    uint32_t he = (uint32_t)(e + 15) + (q >> 11);
+    if (he >= 0x1fu) return (uint16_t)(sign | 0x7c00u);
+    return (uint16_t)(sign | (he << 10) | (q & 0x3ffu));
 }
 
 float fo_fp16_decode(uint16_t bits) {                /* quantize_linear_utils.h:50-68 */
@@ -187,7 +215,7 @@ int fo_cast_from_fp8(int fp8_dtype, const uint8_t* src, float in_scale, int64_t 
         switch (dst_dtype) {
             case FO_FP32: ((float*)out)[i] = v; break;
             case FO_BF16: ((uint16_t*)out)[i] = fo_bf16_encode(v); break;
-            case FO_FP16: ((uint16_t*)out)[i] = fo_fp16_encode(v); break;
+            case FO_FP16: ((uint16_t*)out)[i] = fo_fp16_encode_cast(v); break;
             default: return -1;
         }
     }

@@ -37,7 +37,8 @@ float   fo_fp8_decode(int dtype, uint8_t code);         /* include/util/fp8.h:15
 uint16_t fo_bf16_encode(float value);                   /* include/util/bf16.h:36-46 (NaN quieted) */
 float    fo_bf16_decode(uint16_t bits);                 /* include/util/bf16.h:27-32 */
 uint16_t fo_bf16_encode_plain(float value);             /* quantize_linear_utils.h:110-117 (no NaN quieting) */
-uint16_t fo_fp16_encode(float value);                   /* quantize_linear_utils.h:70-101 */
+uint16_t fo_fp16_encode(float value);                   /* quantize_linear_utils.h:70-101 (DequantizeLinear) */
+uint16_t fo_fp16_encode_cast(float value);              /* include/util/fp16.h FloatToHalf (Cast) */
 float    fo_fp16_decode(uint16_t bits);                 /* quantize_linear_utils.h:50-68 */
 
 /* Vectorised codecs for the tests (count elements). */
@@ -45,6 +46,8 @@ void fo_fp8_encode_array(int dtype, const float* in, uint8_t* out, int64_t count
 void fo_fp8_encode_bits_range(int dtype, uint32_t first_bits, int64_t count, uint8_t* out);
 void fo_bf16_encode_array(const float* in, uint16_t* out, int64_t count);
 void fo_bf16_encode_bits_range(uint32_t first_bits, int64_t count, uint16_t* out);
+/* cast_rule 1: fo_fp16_encode_cast (Cast), 0: fo_fp16_encode (DequantizeLinear) */
+void fo_fp16_encode_bits_range(int cast_rule, uint32_t first_bits, int64_t count, uint16_t* out);
 
 /* ---- Cast (src/kernel/common/cast.cc:62-165) ------------------------------------------ */
 /* bf16/fp32 -> fp8 code with the output scale: code = Enc(x / out_scale). */

@@ -8,6 +8,8 @@
 // Reference code called through this shim:
 //   include/util/fp8.h:66-211            FloatToFp8E4M3/E5M2, Fp8E4M3/E5M2ToFloat
 //   include/util/bf16.h:27-46            FloatToBFloat16
+//   include/util/fp16.h                  FloatToHalf (the Cast operator's FP16 encoder)
+//   src/kernel/common/quantize_linear_utils.h:70-101   EncodeFloat16 (DequantizeLinear's FP16 encoder)
 //   include/quant/quantization.h:94-99   QuantizeInt8Value
 //   src/kernel/common/int8_kernel_utils.h:155-179   QuantizeReal / QuantizeAccumulator
 //   src/kernel/x86/linear_fp8.{h,cc}     ComputeLinearRowMajorX86Fp8{,PackedRhs,TransposedRhs,
@@ -20,8 +22,10 @@
 
 #include "util/fp8.h"
 #include "util/bf16.h"
+#include "util/fp16.h"
 #include "quant/quantization.h"
 #include "src/kernel/common/int8_kernel_utils.h"
+#include "src/kernel/common/quantize_linear_utils.h"
 #include "src/kernel/x86/linear_fp8.h"
 #include "src/kernel/x86/linear.h"
 
@@ -85,6 +89,14 @@ float ref_fp8_decode(int dtype, uint8_t code) {
 
 void ref_bf16_encode_bits_range(uint32_t first_bits, int64_t count, uint16_t* out) {
     for (int64_t i = 0; i < count; ++i) out[i] = feather::FloatToBFloat16(FromBits(first_bits + static_cast<uint32_t>(i)));
+}
+
+// cast_rule 1: FloatToHalf (Cast); 0: EncodeFloat16 (DequantizeLinear)
+void ref_fp16_encode_bits_range(int cast_rule, uint32_t first_bits, int64_t count, uint16_t* out) {
+    for (int64_t i = 0; i < count; ++i) {
+        const float x = FromBits(first_bits + static_cast<uint32_t>(i));
+        out[i] = cast_rule ? feather::FloatToHalf(x) : feather::kernel::quantize_linear_detail::EncodeFloat16(x);
+    }
 }
 
 void ref_quantize_int8_values(const float* in, int64_t count, float scale, int32_t zero_point, int8_t* out) {

@@ -2,7 +2,7 @@
 
 The outputs come from oracle/_ref/libfeather_ref.so, which `make -C oracle ref` compiles from the Feather
 sources themselves: include/util/fp8.h (FloatToFp8E4M3/E5M2, Fp8*ToFloat), include/util/bf16.h
-(FloatToBFloat16), include/quant/quantization.h (QuantizeInt8Value), src/kernel/common/int8_kernel_utils.h
+(FloatToBFloat16), include/util/fp16.h (FloatToHalf, Cast's FP16 rule), quantize_linear_utils.h (EncodeFloat16), include/quant/quantization.h (QuantizeInt8Value), src/kernel/common/int8_kernel_utils.h
 (QuantizeAccumulator), src/kernel/x86/linear_fp8.cc (ComputeLinearRowMajorX86Fp8*, the packed
 TransposedRhsArgmax) and src/kernel/x86/linear.cc (the packed BF16 argmax).  Only inputs and the
 reference's outputs are stored, so the oracle and the HIP path can be checked against the reference
@@ -48,6 +48,12 @@ def make_codec(R):
         R.ref_bf16_encode_bits_range(b, 1, po._ptr(one16))
         bf[i] = one16[0]
     out["bf16_encode"] = bf
+    for name, rule in (("fp16_cast_encode", 1), ("fp16_dequant_encode", 0)):
+        h = np.empty(bits.size, np.uint16)
+        for i, b in enumerate(bits.tolist()):
+            R.ref_fp16_encode_bits_range(rule, b, 1, po._ptr(one16))
+            h[i] = one16[0]
+        out[name] = h
     return out
 
 

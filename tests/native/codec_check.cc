@@ -22,6 +22,7 @@ int main() {
         if (fhip::bf16_encode(x) != fo_bf16_encode(x)) { if (bad < 4) std::printf("bf16 %08llx\n", i); ++bad; }
         if (fhip::bf16_encode_plain(x) != fo_bf16_encode_plain(x)) { if (bad < 4) std::printf("bf16p %08llx\n", i); ++bad; }
         if (fhip::fp16_encode(x) != fo_fp16_encode(x)) { if (bad < 4) std::printf("fp16 %08llx\n", i); ++bad; }
+        if (fhip::fp16_encode_cast(x) != fo_fp16_encode_cast(x)) { if (bad < 4) std::printf("fp16c %08llx\n", i); ++bad; }
     }
     for (int c = 0; c < 256; ++c)
         for (int d = 12; d <= 13; ++d)

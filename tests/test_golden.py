@@ -40,6 +40,22 @@ def test_oracle_bf16_codec_matches_golden():
     assert np.array_equal(po.bf16_encode(codec_bits().view(np.float32)), g["bf16_encode"])
 
 
+def test_oracle_fp16_codecs_match_golden():
+    """Cast's FP16 rule (FloatToHalf: half away from zero) and DequantizeLinear's (EncodeFloat16: RNE)."""
+    g = golden("codec")
+    L = po.lib()
+    bits = codec_bits()
+    one = np.empty(1, np.uint16)
+    for key, rule in (("fp16_cast_encode", 1), ("fp16_dequant_encode", 0)):
+        # through the bit-pattern entry point: a Python float would quiet signalling-NaN inputs
+        got = np.empty(bits.size, np.uint16)
+        for i, b in enumerate(bits.tolist()):
+            L.fo_fp16_encode_bits_range(rule, b, 1, po._ptr(one))
+            got[i] = one[0]
+        assert np.array_equal(got, g[key]), key
+    assert not np.array_equal(g["fp16_cast_encode"], g["fp16_dequant_encode"])  # the two rules do differ
+
+
 def test_oracle_quantize_matches_golden():
     g = golden("quant")
     x = g["q_x"]

@@ -55,6 +55,15 @@ def test_cast_bf16_matches_golden(ctx):
     assert np.array_equal(out.cpu().numpy().view(np.uint16), g["bf16_encode"])
 
 
+def test_cast_fp16_matches_golden(ctx):
+    """Cast to FP16 follows FloatToHalf (half away from zero), not DequantizeLinear's RNE encoder."""
+    g = golden("codec")
+    x = dev(codec_bits().view(np.float32))
+    out = torch.empty(x.numel(), dtype=torch.int16, device="cuda")
+    ctx.cast(x, po.FP32, 1.0, out, po.FP16, 1.0)
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), g["fp16_cast_encode"])
+
+
 def test_quantize_linear_matches_golden(ctx):
     g = golden("quant")
     x = dev(g["q_x"])
