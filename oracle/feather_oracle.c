@@ -132,6 +132,10 @@ void fo_fp16_encode_bits_range(int cast_rule, uint32_t first_bits, int64_t count
     }
 }
 
+void fo_bf16_plain_encode_bits_range(uint32_t first_bits, int64_t count, uint16_t* out) {
+    for (int64_t i = 0; i < count; ++i) out[i] = fo_bf16_encode_plain(u2f(first_bits + (uint32_t)i));
+}
+
 uint16_t fo_bf16_encode_plain(float value) {         /* quantize_linear_utils.h:110-117 */
     uint32_t u = f2u(value);
     uint32_t low = u & 0xffffu, high = u >> 16;

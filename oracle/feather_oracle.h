@@ -46,6 +46,7 @@ void fo_fp8_encode_array(int dtype, const float* in, uint8_t* out, int64_t count
 void fo_fp8_encode_bits_range(int dtype, uint32_t first_bits, int64_t count, uint8_t* out);
 void fo_bf16_encode_array(const float* in, uint16_t* out, int64_t count);
 void fo_bf16_encode_bits_range(uint32_t first_bits, int64_t count, uint16_t* out);
+void fo_bf16_plain_encode_bits_range(uint32_t first_bits, int64_t count, uint16_t* out);
 /* cast_rule 1: fo_fp16_encode_cast (Cast), 0: fo_fp16_encode (DequantizeLinear) */
 void fo_fp16_encode_bits_range(int cast_rule, uint32_t first_bits, int64_t count, uint16_t* out);
 

@@ -52,6 +52,7 @@ def lib():
         _sig(L, "fo_fp16_decode", _F, ctypes.c_uint16)
         _sig(L, "fo_fp16_encode_cast", ctypes.c_uint16, _F)
         _sig(L, "fo_fp16_encode_bits_range", None, _INT, ctypes.c_uint32, _I64, _P)
+        _sig(L, "fo_bf16_plain_encode_bits_range", None, ctypes.c_uint32, _I64, _P)
         _sig(L, "fo_fp8_encode_array", None, _INT, _P, _P, _I64)
         _sig(L, "fo_bf16_encode_array", None, _P, _P, _I64)
         _sig(L, "fo_fp8_encode_bits_range", None, _INT, ctypes.c_uint32, _I64, _P)
@@ -91,6 +92,8 @@ def ref():
         _sig(R, "ref_fp8_decode", _F, _INT, ctypes.c_uint8)
         _sig(R, "ref_bf16_encode_bits_range", None, ctypes.c_uint32, _I64, _P)
         _sig(R, "ref_fp16_encode_bits_range", None, _INT, ctypes.c_uint32, _I64, _P)
+        _sig(R, "ref_bf16_plain_encode_bits_range", None, ctypes.c_uint32, _I64, _P)
+        _sig(R, "ref_fp16_decode", _F, _INT, ctypes.c_uint16)
         _sig(R, "ref_quantize_int8_values", None, _P, _I64, _F, _I32, _P)
         _sig(R, "ref_requantize", _INT, _P, _I64, _I64, _F, _P, _I64, _F, _I32, _P)
         _sig(R, "ref_fp8_linear", _INT, _INT, _P, _F, _P, _F, _INT, _P, _F, _INT, _F, _F, _I64, _I64, _I64, _P, _F)

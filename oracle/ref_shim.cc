@@ -99,6 +99,17 @@ void ref_fp16_encode_bits_range(int cast_rule, uint32_t first_bits, int64_t coun
     }
 }
 
+// EncodeBFloat16 (DequantizeLinear's BF16 encoder: RNE, NaN not quieted)
+void ref_bf16_plain_encode_bits_range(uint32_t first_bits, int64_t count, uint16_t* out) {
+    for (int64_t i = 0; i < count; ++i)
+        out[i] = feather::kernel::quantize_linear_detail::EncodeBFloat16(FromBits(first_bits + static_cast<uint32_t>(i)));
+}
+
+// FP16 decoders: decode_rule 1 = HalfToFloat (Cast, kernel_io), 0 = DecodeFloat16 (QuantizeLinear input)
+float ref_fp16_decode(int decode_rule, uint16_t bits) {
+    return decode_rule ? feather::HalfToFloat(bits) : feather::kernel::quantize_linear_detail::DecodeFloat16(bits);
+}
+
 void ref_quantize_int8_values(const float* in, int64_t count, float scale, int32_t zero_point, int8_t* out) {
     for (int64_t i = 0; i < count; ++i) out[i] = feather::QuantizeInt8Value(in[i], scale, zero_point);
 }

@@ -86,10 +86,11 @@ def test_fp8_encode_round_trip_and_rounding_brute_force():
 
 
 @pytest.mark.skipif(not po.ref_available(), reason="reference build (oracle/_ref) not present")
-@pytest.mark.parametrize("kind", ["e4m3", "e5m2", "bf16", "fp16_cast", "fp16_dequant"])
+@pytest.mark.parametrize("kind", ["e4m3", "e5m2", "bf16", "bf16_plain", "fp16_cast", "fp16_dequant"])
 def test_exhaustive_against_reference_codec(kind):
     """All 2^32 float inputs: the oracle's encoders against the reference's own -- FloatToFp8E4M3/E5M2,
-    FloatToBFloat16, FloatToHalf (Cast's FP16 rule) and EncodeFloat16 (DequantizeLinear's FP16 rule)."""
+    FloatToBFloat16, EncodeBFloat16 (DequantizeLinear's BF16 rule, no NaN quieting), FloatToHalf (Cast's FP16
+    rule) and EncodeFloat16 (DequantizeLinear's FP16 rule)."""
     L, R = po.lib(), po.ref()
     chunk = 1 << 24
 
@@ -99,6 +100,11 @@ def test_exhaustive_against_reference_codec(kind):
             b = np.empty(chunk, np.uint16)
             L.fo_bf16_encode_bits_range(i * chunk, chunk, po._ptr(a))
             R.ref_bf16_encode_bits_range(i * chunk, chunk, po._ptr(b))
+        elif kind == "bf16_plain":
+            a = np.empty(chunk, np.uint16)
+            b = np.empty(chunk, np.uint16)
+            L.fo_bf16_plain_encode_bits_range(i * chunk, chunk, po._ptr(a))
+            R.ref_bf16_plain_encode_bits_range(i * chunk, chunk, po._ptr(b))
         elif kind.startswith("fp16"):
             rule = 1 if kind == "fp16_cast" else 0
             a = np.empty(chunk, np.uint16)
@@ -116,6 +122,13 @@ def test_exhaustive_against_reference_codec(kind):
     with ThreadPoolExecutor(8) as ex:
         bad = sum(ex.map(run, range(256)))
     assert bad == 0
+    if kind.startswith("fp16"):  # both FP16 decoders on every code
+        for h in range(1 << 16):
+            x = np.float32(L.fo_fp16_decode(h))
+            for rule in (0, 1):
+                y = np.float32(R.ref_fp16_decode(rule, h))
+                assert x.tobytes() == y.tobytes() or (np.isnan(x) and np.isnan(y) and
+                                                      (x.view(np.uint32) & 0xFFBFFFFF) == (y.view(np.uint32) & 0xFFBFFFFF)), hex(h)
     if kind in ("e4m3", "e5m2"):
         d = E4 if kind == "e4m3" else E5
         for c in range(256):
