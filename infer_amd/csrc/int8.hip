@@ -300,23 +300,71 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
             bf[j] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
         }
     };
+    // Epilogue parameters (per-channel scale, weight sum, bias) are requested before anything else.
+    float e_scale[WNF];
+    int32_t e_wsum[WNF], e_bias[WNF];
+#pragma unroll
+    for (int j = 0; j < WNF; ++j) {
+        int64_t oc = oc_base + j * 16 + (lane & 15);
+        oc = oc < oc_total ? oc : oc_total - 1;
+        e_scale[j] = ep.w_scales[oc];
+        e_wsum[j] = ep.wsum[oc];
+        e_bias[j] = bias ? bias[oc] : 0;
+    }
+    const int ix0 = (int)(ox0 * g.sw - g.pw);
+    const uint8_t zp = (uint8_t)g.zp_in;
+    // NCHW fast path: rows 4-byte aligned, one (ky, channel) row segment per thread, <= 72 bytes wide.
+    const bool dword_rows = g.layout == FHIP_NCHW && (g.w & 3) == 0 &&
+                            (reinterpret_cast<uintptr_t>(in) & 3) == 0 && wx <= 4 * kWinDwords && g.kh * 64 <= 256;
     for (int64_t c0 = 0; c0 < g.c; c0 += 64) {
-        // weight fragments of every tap are requested first, so they arrive while the window is staged
+        // 1. issue this thread's window loads (fast path), then every tap's weight fragments; nothing
+        //    waits until the LDS writes below, so all of them are in flight together
+        uint32_t d[kWinDwords + 1];
+        int sh = 0;
+        bool row_live = false;
+        if (dword_rows) {
+            const int ci = tid & 63, ky = tid >> 6;
+            const int iy = (int)(oy * g.sh - g.ph) + ky * (int)g.dh;
+            row_live = tid < g.kh * 64 && iy >= 0 && iy < (int)g.h;
+            const uint8_t* row = reinterpret_cast<const uint8_t*>(in) +
+                                 ((b * g.c + c0 + (row_live ? ci : 0)) * g.h + (row_live ? iy : 0)) * g.w;
+            const int a0 = ix0 & ~3;  // floor to a multiple of 4 (two's complement)
+            sh = ix0 - a0;
+#pragma unroll
+            for (int i = 0; i <= kWinDwords; ++i) {
+                const int off = a0 + 4 * i;
+                // a dword is either inside the row or entirely padding (rows are 4-byte aligned);
+                // padding dwords read the row's first dword and are replaced below
+                const bool in_row = off >= 0 && off < (int)g.w;
+                d[i] = *reinterpret_cast<const uint32_t*>(row + (in_row ? off : 0));
+                if (!(in_row && row_live)) d[i] = (uint32_t)zp * 0x01010101u;
+            }
+        }
         v4i bpre[TAPS > 0 ? TAPS : 1][WNF];
         if constexpr (TAPS > 0) {
 #pragma unroll
             for (int t = 0; t < TAPS; ++t) load_b(t, c0, bpre[t]);
         }
-        __syncthreads();
-        // stage the window
-        if (g.layout == FHIP_NCHW) {
-            // thread (ky, ci) copies one input row segment: wx bytes, transposed to channel-last in LDS.
-            // Index math is per row, not per byte; the column loop is pointer increments only.
-            const int ix0 = (int)(ox0 * g.sw - g.pw);
+        // 2. the previous chunk's taps must be done with the window before it is overwritten
+        if (c0 > 0) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+        }
+        // 3. stage the window (channel-last in LDS)
+        if (dword_rows) {
+            if (tid < g.kh * 64) {
+                uint8_t* dst = win + (tid >> 6) * wx * kConvPitch + (tid & 63);
+#pragma unroll
+                for (int i = 0; i < kWinDwords; ++i) {
+                    const uint32_t e = __builtin_amdgcn_alignbyte(d[i + 1], d[i], (uint32_t)sh);
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        if (4 * i + u < wx) dst[(4 * i + u) * kConvPitch] = (uint8_t)(e >> (8 * u));
+                }
+            }
+        } else if (g.layout == FHIP_NCHW) {
+            // byte path: thread (ky, ci) copies one input row segment, transposed to channel-last
             const bool interior = ix0 >= 0 && ix0 + wx <= (int)g.w;  // block-uniform
-            const bool dword_rows = (g.w & 3) == 0 && (reinterpret_cast<uintptr_t>(in) & 3) == 0 &&
-                                    wx <= 4 * kWinDwords;
-            const uint8_t zp = (uint8_t)g.zp_in;
             for (int r = tid; r < (int)g.kh * 64; r += 256) {
                 const int ci = r & 63, ky = r >> 6;
                 const int iy = (int)(oy * g.sh - g.ph) + ky * (int)g.dh;
@@ -326,28 +374,7 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
                     continue;
                 }
                 const uint8_t* row = reinterpret_cast<const uint8_t*>(in) + ((b * g.c + c0 + ci) * g.h + iy) * g.w;
-                if (dword_rows) {
-                    // rows are 4-byte aligned: the whole segment arrives as kWinDwords aligned dword loads in
-                    // flight together; a dword is either inside the row or entirely padding.
-                    const int a0 = ix0 & ~3;  // floor to a multiple of 4 (two's complement)
-                    const int sh = ix0 - a0;
-                    const uint32_t z4 = (uint32_t)zp * 0x01010101u;
-                    uint32_t d[kWinDwords + 1];
-#pragma unroll
-                    for (int i = 0; i <= kWinDwords; ++i) {
-                        const int off = a0 + 4 * i;
-                        d[i] = z4;
-                        if (4 * i < sh + wx && off >= 0 && off < (int)g.w)
-                            d[i] = *reinterpret_cast<const uint32_t*>(row + off);
-                    }
-#pragma unroll
-                    for (int i = 0; i < kWinDwords; ++i) {
-                        const uint32_t e = __builtin_amdgcn_alignbyte(d[i + 1], d[i], (uint32_t)sh);
-#pragma unroll
-                        for (int u = 0; u < 4; ++u)
-                            if (4 * i + u < wx) dst[(4 * i + u) * kConvPitch] = (uint8_t)(e >> (8 * u));
-                    }
-                } else if (interior) {
+                if (interior) {
                     const uint8_t* src = row + ix0;
                     int x = 0;
                     for (; x + 8 <= wx; x += 8) {
@@ -429,20 +456,21 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
         for (int j = 0; j < WNF; ++j) {
             const int64_t oc = oc_base + j * 16 + (lane & 15);
             if (oc >= oc_total) continue;
-            const double scale = (double)ep.s_a * (double)ep.w_scales[oc];
-            const int32_t shift = (bias ? bias[oc] : 0) - (int32_t)g.zp_in * ep.wsum[oc];
+            const double scale = (double)ep.s_a * (double)e_scale[j];
+            const int32_t shift = e_bias[j] - (int32_t)g.zp_in * e_wsum[j];
             int8_t q[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const double real = (double)(acc[f][j][r] + shift) * scale;
                 q[r] = clamp_round_i8(real / ep.inv_out_den + ep.zp_out);
             }
+            const uint32_t packed = (uint32_t)(uint8_t)q[0] | ((uint32_t)(uint8_t)q[1] << 8) |
+                                    ((uint32_t)(uint8_t)q[2] << 16) | ((uint32_t)(uint8_t)q[3] << 24);
             const int64_t ox = ox0 + f * 16 + (lane >> 4) * 4;
             if (g.layout == FHIP_NCHW) {
                 int8_t* dst = ep.out + ((b * oc_total + oc) * g.oh + oy) * g.ow + ox;
                 if (ox + 3 < g.ow && ((reinterpret_cast<uintptr_t>(dst) & 3) == 0)) {
-                    *reinterpret_cast<uint32_t*>(dst) = (uint32_t)(uint8_t)q[0] | ((uint32_t)(uint8_t)q[1] << 8) |
-                                                        ((uint32_t)(uint8_t)q[2] << 16) | ((uint32_t)(uint8_t)q[3] << 24);
+                    *reinterpret_cast<uint32_t*>(dst) = packed;
                 } else {
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
