@@ -268,7 +268,10 @@ __global__ __launch_bounds__(256) void i8_conv_kernel(const int8_t* __restrict__
 // order differs from the reference's (ci, ky, kx) order without changing any sum.
 constexpr int kConvTox = 32;
 constexpr int kConvPitch = 80;  // 64 channels + 16 bytes: stride-2 fragment reads spread over banks
-constexpr int kWinDwords = 18;  // NCHW rows staged by aligned dword loads when the window is <= 72 bytes
+// NCHW fast staging: a thread covers kWinCols window columns of 4 channels, kWinSpan aligned dwords per
+// channel (the columns plus up to 3 bytes of alignment shift); windows up to 4 * kWinCols = 80 columns.
+constexpr int kWinCols = 20;
+constexpr int kWinSpan = kWinCols / 4 + 1;
 
 template <int WNF, int TAPS>
 __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __restrict__ in, ConvGeom g,
@@ -313,31 +316,36 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
     }
     const int ix0 = (int)(ox0 * g.sw - g.pw);
     const uint8_t zp = (uint8_t)g.zp_in;
-    // NCHW fast path: rows 4-byte aligned, one (ky, channel) row segment per thread, <= 72 bytes wide.
+    // NCHW fast path: rows 4-byte aligned, at most 4 tap rows, a window of at most 80 columns.
     const bool dword_rows = g.layout == FHIP_NCHW && (g.w & 3) == 0 &&
-                            (reinterpret_cast<uintptr_t>(in) & 3) == 0 && wx <= 4 * kWinDwords && g.kh * 64 <= 256;
+                            (reinterpret_cast<uintptr_t>(in) & 3) == 0 && wx <= 4 * kWinCols && g.kh * 64 <= 256;
     for (int64_t c0 = 0; c0 < g.c; c0 += 64) {
         // 1. issue this thread's window loads (fast path), then every tap's weight fragments; nothing
         //    waits until the LDS writes below, so all of them are in flight together
-        uint32_t d[kWinDwords + 1];
+        // thread t: tap row ky = t / 64, channels 4*cq .. 4*cq+3 with cq = (t / 4) % 16, window columns
+        // [20*xq, 20*xq + 20) with xq = t % 4; per channel the columns come as kWinSpan aligned dwords
+        uint32_t d[4][kWinSpan];
         int sh = 0;
-        bool row_live = false;
         if (dword_rows) {
-            const int ci = tid & 63, ky = tid >> 6;
+            const int ky = tid >> 6, cq = (tid >> 2) & 15, xq = tid & 3;
             const int iy = (int)(oy * g.sh - g.ph) + ky * (int)g.dh;
-            row_live = tid < g.kh * 64 && iy >= 0 && iy < (int)g.h;
-            const uint8_t* row = reinterpret_cast<const uint8_t*>(in) +
-                                 ((b * g.c + c0 + (row_live ? ci : 0)) * g.h + (row_live ? iy : 0)) * g.w;
-            const int a0 = ix0 & ~3;  // floor to a multiple of 4 (two's complement)
-            sh = ix0 - a0;
+            const bool row_live = tid < g.kh * 64 && iy >= 0 && iy < (int)g.h;
+            const int gx = ix0 + xq * kWinCols;       // first input column of this thread
+            const int a0 = gx & ~3;                   // floor to a multiple of 4 (two's complement)
+            sh = gx - a0;
 #pragma unroll
-            for (int i = 0; i <= kWinDwords; ++i) {
-                const int off = a0 + 4 * i;
-                // a dword is either inside the row or entirely padding (rows are 4-byte aligned);
-                // padding dwords read the row's first dword and are replaced below
-                const bool in_row = off >= 0 && off < (int)g.w;
-                d[i] = *reinterpret_cast<const uint32_t*>(row + (in_row ? off : 0));
-                if (!(in_row && row_live)) d[i] = (uint32_t)zp * 0x01010101u;
+            for (int c = 0; c < 4; ++c) {
+                const uint8_t* row = reinterpret_cast<const uint8_t*>(in) +
+                                     ((b * g.c + c0 + (row_live ? 4 * cq + c : 0)) * g.h + (row_live ? iy : 0)) * g.w;
+#pragma unroll
+                for (int i = 0; i < kWinSpan; ++i) {
+                    const int off = a0 + 4 * i;
+                    // a dword is either inside the row or entirely padding (rows are 4-byte aligned);
+                    // padding dwords read the row's first dword and are replaced below
+                    const bool in_row = off >= 0 && off < (int)g.w;
+                    d[c][i] = *reinterpret_cast<const uint32_t*>(row + (in_row ? off : 0));
+                    if (!(in_row && row_live)) d[c][i] = (uint32_t)zp * 0x01010101u;
+                }
             }
         }
         v4i bpre[TAPS > 0 ? TAPS : 1][WNF];
@@ -353,13 +361,26 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
         // 3. stage the window (channel-last in LDS)
         if (dword_rows) {
             if (tid < g.kh * 64) {
-                uint8_t* dst = win + (tid >> 6) * wx * kConvPitch + (tid & 63);
+                const int ky = tid >> 6, cq = (tid >> 2) & 15, x0 = (tid & 3) * kWinCols;
+                uint8_t* dst = win + (ky * wx + x0) * kConvPitch + 4 * cq;
 #pragma unroll
-                for (int i = 0; i < kWinDwords; ++i) {
-                    const uint32_t e = __builtin_amdgcn_alignbyte(d[i + 1], d[i], (uint32_t)sh);
+                for (int i = 0; i < kWinCols / 4; ++i) {
+                    // e[c] holds columns x0+4i .. +3 of channel c; a 4x4 byte transpose gives, per column,
+                    // the four channels as one dword (v_perm_b32: bytes 0-3 = second operand)
+                    uint32_t e[4];
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) e[c] = __builtin_amdgcn_alignbyte(d[c][i + 1], d[c][i], (uint32_t)sh);
+                    const uint32_t lo01 = __builtin_amdgcn_perm(e[1], e[0], 0x05010400u);
+                    const uint32_t hi01 = __builtin_amdgcn_perm(e[1], e[0], 0x07030602u);
+                    const uint32_t lo23 = __builtin_amdgcn_perm(e[3], e[2], 0x05010400u);
+                    const uint32_t hi23 = __builtin_amdgcn_perm(e[3], e[2], 0x07030602u);
+                    const uint32_t col[4] = {__builtin_amdgcn_perm(lo23, lo01, 0x05040100u),
+                                             __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
+                                             __builtin_amdgcn_perm(hi23, hi01, 0x05040100u),
+                                             __builtin_amdgcn_perm(hi23, hi01, 0x07060302u)};
 #pragma unroll
                     for (int u = 0; u < 4; ++u)
-                        if (4 * i + u < wx) dst[(4 * i + u) * kConvPitch] = (uint8_t)(e >> (8 * u));
+                        if (x0 + 4 * i + u < wx) *reinterpret_cast<uint32_t*>(dst + (4 * i + u) * kConvPitch) = col[u];
                 }
             }
         } else if (g.layout == FHIP_NCHW) {
