@@ -127,6 +127,14 @@ int fhip_fp8_linear(fhip_context ctx, int a_dtype, const void* a, float a_scale,
 int fhip_i8_linear(fhip_context ctx, int kind, const int8_t* a, float s_a, int32_t zp_a, int64_t m, fhip_weight w,
                    const int32_t* bias, int bias_kind, int32_t bias_abs_max, float alpha, float beta, int8_t* out,
                    float s_out, int32_t zp_out);
+/* The same INT8 linear followed by the graph's DequantizeLinear of its output, in one launch
+ * (common/quantize_linear_utils.h:291-341, per tensor): out_dtype FHIP_INT8 is fhip_i8_linear;
+ * FHIP_FP32 / FHIP_FP16 / FHIP_BF16 write float((q - dq_zp) * dq_scale) encoded as DequantizeLinear does,
+ * where q is the INT8 result fhip_i8_linear would write (out_scale / out_zp).  Equal, value for value, to
+ * the two nodes run one after the other (the Q -> Gemm -> DQ chain of the INT8 export). */
+int fhip_i8_linear_ex(fhip_context ctx, int kind, const int8_t* a, float s_a, int32_t zp_a, int64_t m, fhip_weight w,
+                      const int32_t* bias, int bias_kind, int32_t bias_abs_max, float alpha, float beta, int out_dtype,
+                      void* out, float s_out, int32_t zp_out, float dq_scale, int32_t dq_zp);
 
 /* ---- INT8 Conv2D as implicit GEMM (common/conv2d.cc:482-581; x86/int8.cc:684-2346) ------- */
 int fhip_i8_conv2d(fhip_context ctx, const int8_t* in, int64_t n, int64_t c, int64_t h, int64_t w, int layout,

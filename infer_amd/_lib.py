@@ -45,6 +45,8 @@ SIGNATURES = {
     "fhip_cast": (_INT, [_P, _INT, _P, _F, _I64, _INT, _P, _F]),
     "fhip_fp8_linear": (_INT, [_P, _INT, _P, _F, _I64, _P, _F, _P, _F, _INT, _F, _F, _INT, _P, _F]),
     "fhip_i8_linear": (_INT, [_P, _INT, _P, _F, _I32, _I64, _P, _P, _INT, _I32, _F, _F, _P, _F, _I32]),
+    "fhip_i8_linear_ex": (_INT, [_P, _INT, _P, _F, _I32, _I64, _P, _P, _INT, _I32, _F, _F, _INT, _P, _F, _I32, _F,
+                                 _I32]),
     "fhip_i8_conv2d": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _INT, _F, _I32, _P, _P, _I32, _I32, _I32, _I32, _I32,
                               _I32, _I32, _P, _I64, _I64, _F, _I32]),
     "fhip_quantize_linear": (_INT, [_P, _INT, _P, _I64, _I64, _I64, _P, _P, _I64, _P]),

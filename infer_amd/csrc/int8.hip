@@ -45,6 +45,12 @@ struct I8Epilogue {
     double zp_out;
     int8_t* out;
     int64_t ldo;
+    // Fused DequantizeLinear (per tensor): out_dtype FP32/FP16/BF16 writes float((q - dq_zp) * dq_scale) with
+    // DequantizeLinear's own encoders into out_any instead of the INT8 code q into out.
+    int out_dtype = FHIP_INT8;
+    float dq_scale = 1.0f;
+    int32_t dq_zp = 0;
+    void* out_any = nullptr;
 
     __device__ __forceinline__ void store(int32_t raw, int64_t row, int64_t col) const {
         const int32_t dot = raw - zp_a * wsum[col];
@@ -57,7 +63,16 @@ struct I8Epilogue {
         } else {
             real = (double)(dot + b) * scale;  // MatMul has no bias (b = 0)
         }
-        out[row * ldo + col] = clamp_round_i8(real / inv_out_den + zp_out);
+        const int8_t q = clamp_round_i8(real / inv_out_den + zp_out);
+        const int64_t idx = row * ldo + col;
+        if (out_dtype == FHIP_INT8) {
+            out[idx] = q;
+        } else {
+            const float v = (float)((int32_t)q - dq_zp) * dq_scale;  // quantize_linear_utils.h:291-341
+            if (out_dtype == FHIP_FP32) static_cast<float*>(out_any)[idx] = v;
+            else if (out_dtype == FHIP_FP16) static_cast<uint16_t*>(out_any)[idx] = fhip::fp16_encode(v);
+            else static_cast<uint16_t*>(out_any)[idx] = fhip::bf16_encode_plain(v);
+        }
     }
 };
 
@@ -602,7 +617,18 @@ extern "C" {
 int fhip_i8_linear(fhip_context ctx, int kind, const int8_t* a, float s_a, int32_t zp_a, int64_t m, fhip_weight w,
                    const int32_t* bias, int bias_kind, int32_t bias_abs_max, float alpha, float beta, int8_t* out,
                    float s_out, int32_t zp_out) {
+    return fhip_i8_linear_ex(ctx, kind, a, s_a, zp_a, m, w, bias, bias_kind, bias_abs_max, alpha, beta, FHIP_INT8, out,
+                             s_out, zp_out, 1.0f, 0);
+}
+
+int fhip_i8_linear_ex(fhip_context ctx, int kind, const int8_t* a, float s_a, int32_t zp_a, int64_t m, fhip_weight w,
+                      const int32_t* bias, int bias_kind, int32_t bias_abs_max, float alpha, float beta, int out_dtype,
+                      void* out, float s_out, int32_t zp_out, float dq_scale, int32_t dq_zp) {
     if (!ctx) return FHIP_ERR_INVALID;
+    if (out_dtype != FHIP_INT8 && out_dtype != FHIP_FP32 && out_dtype != FHIP_FP16 && out_dtype != FHIP_BF16)
+        return fhip::set_error(ctx, FHIP_ERR_INVALID, "i8_linear: out_dtype must be INT8, FP32, FP16 or BF16");
+    if (out_dtype != FHIP_INT8 && (!fhip::valid_scale(dq_scale) || dq_zp < -128 || dq_zp > 127))
+        return fhip::set_error(ctx, FHIP_ERR_INVALID, "i8_linear: invalid DequantizeLinear parameters");
     if (!a || !w || !out || m <= 0 || w->kind != kLinearWeight || w->dtype != FHIP_INT8 || kind < FHIP_I8_MATMUL ||
         kind > FHIP_I8_GEMM || bias_kind < FHIP_BIAS_NONE || bias_kind > FHIP_BIAS_MATRIX ||
         (bias_kind != FHIP_BIAS_NONE && !bias))
@@ -620,7 +646,11 @@ int fhip_i8_linear(fhip_context ctx, int kind, const int8_t* a, float s_a, int32
                               (double)s_a * (double)w->max_scale / (double)s_out;
     if (!(real_bound < 1e300)) return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "i8_linear: scales too large");
     I8Epilogue ep{kind, w->scales, w->wsum, bias, bias_kind, zp_a, s_a, (double)alpha, (double)beta, (double)s_out,
-                  (double)zp_out, out, w->n};
+                  (double)zp_out, static_cast<int8_t*>(out), w->n};
+    ep.out_dtype = out_dtype;
+    ep.dq_scale = dq_scale;
+    ep.dq_zp = dq_zp;
+    ep.out_any = out;
     const int64_t kp = ((w->k + 127) / 128) * 128;
     // largest tile that still puts about two blocks on every CU
     const int64_t blocks32 = ((w->n + 31) / 32) * ((m + 31) / 32);

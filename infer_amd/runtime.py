@@ -146,6 +146,12 @@ class Context:
         return self._run(self.lib.fhip_i8_linear, kind, _p(a), s_a, zp_a, m, w.handle, _p(bias), bias_kind,
                                      bias_abs_max, alpha, beta, _p(out), s_out, zp_out, check=check)
 
+    def i8_linear_ex(self, kind, a, s_a, zp_a, m, w, out, out_dtype, s_out, zp_out, dq_scale=1.0, dq_zp=0, bias=None,
+                     bias_kind=L.BIAS_NONE, bias_abs_max=0, alpha=1.0, beta=1.0, check=True):
+        """INT8 linear with the following DequantizeLinear fused (out_dtype FP32/FP16/BF16)."""
+        return self._run(self.lib.fhip_i8_linear_ex, kind, _p(a), s_a, zp_a, m, w.handle, _p(bias), bias_kind,
+                         bias_abs_max, alpha, beta, out_dtype, _p(out), s_out, zp_out, dq_scale, dq_zp, check=check)
+
     def i8_conv2d(self, x, layout, s_in, zp_in, w, out, s_out, zp_out, stride=(1, 1), pad=(0, 0), dilation=(1, 1),
                   bias=None, bias_abs_max=0, check=True):
         if layout == L.NCHW:

@@ -99,6 +99,32 @@ def test_i8_linear_config1_bitexact(ctx, kind):
     wt.release()
 
 
+@pytest.mark.parametrize("out_dtype", [po.FP32, po.FP16, po.BF16])
+def test_i8_gemm_fused_dequantize_matches_chain(ctx, out_dtype):
+    """Config 1's Gemm -> DequantizeLinear pair in one launch equals the two nodes run one after the other,
+    bit for bit, including a DequantizeLinear whose parameters differ from the Gemm output's."""
+    x, s_x, w_nk, s_w, bias = c1_inputs()
+    m, k = x.shape
+    n = w_nk.shape[0]
+    _, xq = po.quantize_linear(po.FP32, x, [s_x], [0])
+    wt = ctx.prepare_weight(dev(w_nk), po.INT8, k, n, 1, scales=s_w, version=40)
+    for s_y, zp_y, s_dq, zp_dq in ((0.05, 0, 0.05, 0), (0.0371, -6, 0.0125, 3)):
+        rc, yq, _ = po.i8_linear(po.I8_GEMM, xq, s_x, 0, w_nk, True, s_w, None, bias, po.BIAS_VECTOR, 1.0, 1.0, s_y,
+                                 zp_y)
+        assert rc == 0
+        rc, ref = po.dequantize_linear(yq, [s_dq], [zp_dq], out_dtype)
+        assert rc == 0
+        tdt = torch.float32 if out_dtype == po.FP32 else torch.int16
+        out = torch.empty((m, n), dtype=tdt, device="cuda")
+        ctx.i8_linear_ex(po.I8_GEMM, dev(xq), s_x, 0, m, wt, out, out_dtype, s_y, zp_y, dq_scale=s_dq, dq_zp=zp_dq,
+                         bias=dev(bias), bias_kind=po.BIAS_VECTOR, bias_abs_max=int(np.abs(bias).max()))
+        got = out.cpu().numpy()
+        if out_dtype != po.FP32:
+            got = got.view(np.uint16)
+        assert np.array_equal(got.view(np.uint8), np.ascontiguousarray(ref).view(np.uint8)), (s_y, zp_y)
+    wt.release()
+
+
 def test_i8_gemm_zero_points_alpha_beta_ragged(ctx):
     r = rng(21)
     m, k, n = 37, 80, 45
