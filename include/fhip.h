@@ -62,6 +62,9 @@ typedef struct fhip_weight_s* fhip_weight;
 typedef struct fhip_graph_s* fhip_graph;
 
 /* ---- context (BackendContext, include/core/backend.h:43-96; runtime.h:39-157) ------------ */
+/* Sizes: an empty input (m, count or batch 0) returns FHIP_OK without launching anything -- the
+ * reference's loops run zero times and its kernels return 0; an empty K, N or vocabulary returns
+ * FHIP_ERR_UNSUPPORTED so the caller's Common kernel produces the reference's result. */
 int fhip_version(void);
 /* Creates a context bound to `device` with its own non-blocking stream and a scratch arena. */
 int fhip_context_create(int device, fhip_context* out);

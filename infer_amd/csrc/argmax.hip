@@ -477,7 +477,10 @@ extern "C" {
 int fhip_bf16_gemv_argmax(fhip_context ctx, const uint16_t* a, int64_t m, int64_t k, const uint16_t* w, int64_t v,
                           int64_t* tokens, float* logits) {
     if (!ctx) return FHIP_ERR_INVALID;
-    if (!a || !w || !tokens || m <= 0 || k <= 0 || v <= 0) return fhip::set_error(ctx, FHIP_ERR_INVALID, "bf16_gemv_argmax: bad arguments");
+    if (m == 0) return FHIP_OK;  // no rows: nothing to select (the reference's loops run zero times)
+    if (m > 0 && (k == 0 || v == 0))
+        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "bf16_gemv_argmax: empty K or vocabulary");
+    if (!a || !w || !tokens || m < 0 || k < 0 || v < 0) return fhip::set_error(ctx, FHIP_ERR_INVALID, "bf16_gemv_argmax: bad arguments");
     if (m > kArgmaxMaxRows || (k * 2) % 16 != 0 || k * 2 > 4096 || v >= (int64_t(1) << 32))
         return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "bf16_gemv_argmax: needs m <= 16, k % 8 == 0, k <= 2048");
     if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(w)) & 15)
@@ -490,7 +493,10 @@ int fhip_bf16_gemv_argmax(fhip_context ctx, const uint16_t* a, int64_t m, int64_
 int fhip_fp8_gemv_argmax(fhip_context ctx, int dtype, const uint8_t* a, float a_scale, int64_t m, int64_t k,
                          const uint8_t* w, float w_scale, int64_t v, float out_scale, int64_t* tokens) {
     if (!ctx) return FHIP_ERR_INVALID;
-    if (!a || !w || !tokens || m <= 0 || k <= 0 || v <= 0 || (dtype != FHIP_FP8E4M3 && dtype != FHIP_FP8E5M2))
+    if (m == 0) return FHIP_OK;
+    if (m > 0 && (k == 0 || v == 0))
+        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "fp8_gemv_argmax: empty K or vocabulary");
+    if (!a || !w || !tokens || m < 0 || k < 0 || v < 0 || (dtype != FHIP_FP8E4M3 && dtype != FHIP_FP8E5M2))
         return fhip::set_error(ctx, FHIP_ERR_INVALID, "fp8_gemv_argmax: bad arguments");
     if (!fhip::valid_scale(a_scale) || !fhip::valid_scale(w_scale) || !fhip::valid_scale(out_scale))
         return fhip::set_error(ctx, FHIP_ERR_INVALID, "fp8_gemv_argmax: scales must be finite and positive");

@@ -430,6 +430,7 @@ extern "C" {
 int fhip_cast(fhip_context ctx, int src_dtype, const void* src, float src_scale, int64_t count, int dst_dtype,
               void* dst, float dst_scale) {
     if (!ctx) return FHIP_ERR_INVALID;
+    if (count == 0) return FHIP_OK;  // empty tensor: nothing to convert
     if (!src || !dst || count < 0 || !is_castable(src_dtype) || !is_castable(dst_dtype))
         return fhip::set_error(ctx, FHIP_ERR_INVALID, "cast: bad arguments");
     if ((is_fp8(src_dtype) && !fhip::valid_scale(src_scale)) || (is_fp8(dst_dtype) && !fhip::valid_scale(dst_scale)))
@@ -446,7 +447,8 @@ int fhip_fp8_linear(fhip_context ctx, int a_dtype, const void* a, float a_scale,
                     float w_scale, const uint8_t* bias, float bias_scale, int bias_kind, float alpha, float beta,
                     int out_dtype, void* out, float out_scale) {
     if (!ctx) return FHIP_ERR_INVALID;
-    if (!w || !a || !out || m <= 0 || w->kind != kLinearWeight || !is_fp8(w->dtype))
+    if (m == 0) return FHIP_OK;  // no activation rows: the reference's loops run zero times
+    if (!w || !a || !out || m < 0 || w->kind != kLinearWeight || !is_fp8(w->dtype))
         return fhip::set_error(ctx, FHIP_ERR_INVALID, "fp8_linear: bad arguments");
     if (a_dtype != w->dtype && a_dtype != FHIP_BF16 && a_dtype != FHIP_FP32)
         return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "fp8_linear: activation dtype must match the weight");

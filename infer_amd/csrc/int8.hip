@@ -629,7 +629,8 @@ int fhip_i8_linear_ex(fhip_context ctx, int kind, const int8_t* a, float s_a, in
         return fhip::set_error(ctx, FHIP_ERR_INVALID, "i8_linear: out_dtype must be INT8, FP32, FP16 or BF16");
     if (out_dtype != FHIP_INT8 && (!fhip::valid_scale(dq_scale) || dq_zp < -128 || dq_zp > 127))
         return fhip::set_error(ctx, FHIP_ERR_INVALID, "i8_linear: invalid DequantizeLinear parameters");
-    if (!a || !w || !out || m <= 0 || w->kind != kLinearWeight || w->dtype != FHIP_INT8 || kind < FHIP_I8_MATMUL ||
+    if (m == 0) return FHIP_OK;  // no activation rows: the reference's loops run zero times
+    if (!a || !w || !out || m < 0 || w->kind != kLinearWeight || w->dtype != FHIP_INT8 || kind < FHIP_I8_MATMUL ||
         kind > FHIP_I8_GEMM || bias_kind < FHIP_BIAS_NONE || bias_kind > FHIP_BIAS_MATRIX ||
         (bias_kind != FHIP_BIAS_NONE && !bias))
         return fhip::set_error(ctx, FHIP_ERR_INVALID, "i8_linear: bad arguments");
@@ -673,7 +674,8 @@ int fhip_i8_conv2d(fhip_context ctx, const int8_t* in, int64_t n, int64_t c, int
                    int32_t stride_h, int32_t stride_w, int32_t pad_h, int32_t pad_w, int32_t dil_h, int32_t dil_w,
                    int8_t* out, int64_t oh, int64_t ow, float s_out, int32_t zp_out) {
     if (!ctx) return FHIP_ERR_INVALID;
-    if (!in || !wt || !out || wt->kind != kConvWeight || n <= 0 || c <= 0 || h <= 0 || w <= 0 || stride_h <= 0 ||
+    if (n == 0) return FHIP_OK;  // empty batch
+    if (!in || !wt || !out || wt->kind != kConvWeight || n < 0 || c <= 0 || h <= 0 || w <= 0 || stride_h <= 0 ||
         stride_w <= 0 || dil_h <= 0 || dil_w <= 0 || pad_h < 0 || pad_w < 0 || (layout != FHIP_NCHW && layout != FHIP_NHWC))
         return fhip::set_error(ctx, FHIP_ERR_INVALID, "i8_conv2d: bad arguments");
     if (c != wt->icg * wt->group) return fhip::set_error(ctx, FHIP_ERR_INVALID, "i8_conv2d: channels do not match");
@@ -726,7 +728,8 @@ int fhip_i8_conv2d(fhip_context ctx, const int8_t* in, int64_t n, int64_t c, int
 int fhip_quantize_linear(fhip_context ctx, int src_dtype, const void* src, int64_t count, int64_t channels,
                          int64_t inner, const float* scales, const int32_t* zero_points, int64_t n_zp, int8_t* out) {
     if (!ctx) return FHIP_ERR_INVALID;
-    if (!src || !out || count <= 0 || inner <= 0 ||
+    if (count == 0) return FHIP_OK;  // empty tensor
+    if (!src || !out || count < 0 || inner <= 0 ||
         (src_dtype != FHIP_FP32 && src_dtype != FHIP_BF16 && src_dtype != FHIP_FP16))
         return fhip::set_error(ctx, FHIP_ERR_INVALID, "quantize_linear: bad arguments");
     int rc = validate_qparams(ctx, channels, scales, zero_points, n_zp);
@@ -745,7 +748,8 @@ int fhip_quantize_linear(fhip_context ctx, int src_dtype, const void* src, int64
 int fhip_dequantize_linear(fhip_context ctx, const int8_t* src, int64_t count, int64_t channels, int64_t inner,
                            const float* scales, const int32_t* zero_points, int64_t n_zp, int dst_dtype, void* out) {
     if (!ctx) return FHIP_ERR_INVALID;
-    if (!src || !out || count <= 0 || inner <= 0 ||
+    if (count == 0) return FHIP_OK;  // empty tensor
+    if (!src || !out || count < 0 || inner <= 0 ||
         (dst_dtype != FHIP_FP32 && dst_dtype != FHIP_BF16 && dst_dtype != FHIP_FP16))
         return fhip::set_error(ctx, FHIP_ERR_INVALID, "dequantize_linear: bad arguments");
     int rc = validate_qparams(ctx, channels, scales, zero_points, n_zp);

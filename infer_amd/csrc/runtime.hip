@@ -294,6 +294,8 @@ int fhip_weight_prepare(fhip_context ctx, const void* src, int dtype, int64_t k,
     *out = nullptr;
     std::lock_guard<std::recursive_mutex> lock(ctx->mu);
     DeviceGuard guard(ctx->device);
+    if ((k == 0 || n == 0) && src_layout >= FHIP_LAYOUT_KN && src_layout <= FHIP_LAYOUT_NK)
+        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "weight_prepare: empty weight (the Common kernel handles it)");
     if (!src || k <= 0 || n <= 0 || (src_layout != FHIP_LAYOUT_KN && src_layout != FHIP_LAYOUT_NK))
         return set_error(ctx, FHIP_ERR_INVALID, "weight_prepare: bad arguments");
     if (dtype != FHIP_FP8E4M3 && dtype != FHIP_FP8E5M2 && dtype != FHIP_INT8)
