@@ -45,6 +45,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--only-headline", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--configs", default="", help="comma list of extra configs to run (C1..C5; default all)")
     return p.parse_args()
 
 
@@ -208,125 +209,135 @@ def cpu_headline(args):
 def extra_configs(b, args):
     t, L, ctx = b.torch, b.L, b.ctx
     res = {}
+    chosen = set(args.configs.split(",")) if args.configs else None
 
-    # C2 M=4, 16
-    k, n, copies = 1024, 3584, 80
-    w_codes, sw = b.to_fp8(b.randn((k, n), 0xFEA70002, 0.02), L.FP8E4M3)
-    srcs = [w_codes.clone() for _ in range(copies)]
-    weights = [ctx.prepare_weight(s_, L.FP8E4M3, k, n, L.LAYOUT_KN, version=2) for s_ in srcs]
-    for m in (4, 16):
-        xb = b.randn((m, k), 0xFEA70002 + m).to(t.bfloat16)
-        out = t.empty((m, n), dtype=t.bfloat16, device="cuda")
+    def want(tag):
+        return chosen is None or tag in chosen
 
-        def step(i, xb=xb, out=out, m=m):
-            ctx.fp8_linear(xb, L.BF16, 0.0078125, m, weights[i % copies], sw, out, L.BF16, 0.03125)
-        ms, _ = b.graph_time([(lambda i=i: step(i)) for i in range(200)], 5)
-        km, _ = b.kernel_time(step, 200)
-        by = k * n + m * k * 2 + m * n * 2
-        res[f"C2_fp8_decode_M{m}"] = {"ms_per_step": ms, "GB/s": by / ms / 1e6, "kernel_ms": km,
-                                      "kernel_GB/s": by / km / 1e6, "hbm_frac": by / km / 1e6 / HBM_PEAK_GBS}
-    for wt in weights:
-        wt.release()
-    del srcs
+    if want("C2"):
+        # C2 M=4, 16
+        k, n, copies = 1024, 3584, 80
+        w_codes, sw = b.to_fp8(b.randn((k, n), 0xFEA70002, 0.02), L.FP8E4M3)
+        srcs = [w_codes.clone() for _ in range(copies)]
+        weights = [ctx.prepare_weight(s_, L.FP8E4M3, k, n, L.LAYOUT_KN, version=2) for s_ in srcs]
+        for m in (4, 16):
+            xb = b.randn((m, k), 0xFEA70002 + m).to(t.bfloat16)
+            out = t.empty((m, n), dtype=t.bfloat16, device="cuda")
 
-    # C3 FP8 e5m2 prefill: up-proj [4096,1024]x[1024->3584], down-proj [4096,3584]x[3584->1024]
-    m, k, n = 4096, 1024, 3584
-    E5 = L.FP8E5M2
-    a_codes, sa = b.to_fp8(b.randn((m, k), 0xFEA70003), E5)
-    wu_codes, su = b.to_fp8(b.randn((n, k), 0xFEA70003 + 1, 0.02), E5)
-    wd_codes, sd = b.to_fp8(b.randn((k, n), 0xFEA70003 + 2, 0.02), E5)
-    wu = ctx.prepare_weight(wu_codes, E5, k, n, L.LAYOUT_NK, version=3)
-    wd = ctx.prepare_weight(wd_codes, E5, n, k, L.LAYOUT_NK, version=3)
-    mid = t.empty((m, n), dtype=t.uint8, device="cuda")
-    out = t.empty((m, k), dtype=t.bfloat16, device="cuda")
-    s_mid, s_o = 0.125, 0.25
+            def step(i, xb=xb, out=out, m=m):
+                ctx.fp8_linear(xb, L.BF16, 0.0078125, m, weights[i % copies], sw, out, L.BF16, 0.03125)
+            ms, _ = b.graph_time([(lambda i=i: step(i)) for i in range(200)], 5)
+            km, _ = b.kernel_time(step, 200)
+            by = k * n + m * k * 2 + m * n * 2
+            res[f"C2_fp8_decode_M{m}"] = {"ms_per_step": ms, "GB/s": by / ms / 1e6, "kernel_ms": km,
+                                          "kernel_GB/s": by / km / 1e6, "hbm_frac": by / km / 1e6 / HBM_PEAK_GBS}
+        for wt in weights:
+            wt.release()
+        del srcs
 
-    def up(i=0):
-        ctx.fp8_linear(a_codes, E5, sa, m, wu, su, mid, E5, s_mid)
+    if want("C3"):
+        # C3 FP8 e5m2 prefill: up-proj [4096,1024]x[1024->3584], down-proj [4096,3584]x[3584->1024]
+        m, k, n = 4096, 1024, 3584
+        E5 = L.FP8E5M2
+        a_codes, sa = b.to_fp8(b.randn((m, k), 0xFEA70003), E5)
+        wu_codes, su = b.to_fp8(b.randn((n, k), 0xFEA70003 + 1, 0.02), E5)
+        wd_codes, sd = b.to_fp8(b.randn((k, n), 0xFEA70003 + 2, 0.02), E5)
+        wu = ctx.prepare_weight(wu_codes, E5, k, n, L.LAYOUT_NK, version=3)
+        wd = ctx.prepare_weight(wd_codes, E5, n, k, L.LAYOUT_NK, version=3)
+        mid = t.empty((m, n), dtype=t.uint8, device="cuda")
+        out = t.empty((m, k), dtype=t.bfloat16, device="cuda")
+        s_mid, s_o = 0.125, 0.25
 
-    def down(i=0):
-        ctx.fp8_linear(mid, E5, s_mid, m, wd, sd, out, L.BF16, s_o)
-    ms, _ = b.graph_time([up, down] * 10, 5)
-    ku, _ = b.kernel_time(up, 50)
-    kd, _ = b.kernel_time(down, 50)
-    fl = 2.0 * m * k * n
-    res["C3_fp8e5m2_prefill"] = {
-        "ms_per_gemm": ms, "TFLOP/s": fl / ms / 1e9, "mfma_frac": fl / ms / 1e9 / FP8_PEAK_TFLOPS,
-        "up_kernel_ms": ku, "up_TFLOP/s": fl / ku / 1e9, "down_kernel_ms": kd, "down_TFLOP/s": fl / kd / 1e9,
-        "backend": ctx.last_backend()}
-    wu.release()
-    wd.release()
+        def up(i=0):
+            ctx.fp8_linear(a_codes, E5, sa, m, wu, su, mid, E5, s_mid)
 
-    # C1 INT8 linear chain: QuantizeLinear(fp32) -> Gemm INT8 (transB) -> DequantizeLinear(fp32)
-    m, k, n = 128, 1024, 1024
-    x = b.randn((m, k), 0xFEA70001)
-    s_x = float(x.abs().max()) / 127.0
-    b.gen.manual_seed(0xFEA70001 + 1)
-    wq = t.randint(-127, 128, (n, k), generator=b.gen, device="cuda", dtype=t.int8)
-    s_w = (t.rand(n, generator=b.gen, device="cuda") * 9e-3 + 1e-3).cpu().numpy()
-    bias = t.randint(-20000, 20000, (n,), generator=b.gen, device="cuda", dtype=t.int32)
-    w8 = ctx.prepare_weight(wq, L.INT8, k, n, L.LAYOUT_NK, scales=s_w, version=4)
-    xq = t.empty((m, k), dtype=t.int8, device="cuda")
-    yq = t.empty((m, n), dtype=t.int8, device="cuda")
-    y = t.empty((m, n), dtype=t.float32, device="cuda")
-    s_y = 0.05
+        def down(i=0):
+            ctx.fp8_linear(mid, E5, s_mid, m, wd, sd, out, L.BF16, s_o)
+        ms, _ = b.graph_time([up, down] * 10, 5)
+        ku, _ = b.kernel_time(up, 50)
+        kd, _ = b.kernel_time(down, 50)
+        fl = 2.0 * m * k * n
+        res["C3_fp8e5m2_prefill"] = {
+            "ms_per_gemm": ms, "TFLOP/s": fl / ms / 1e9, "mfma_frac": fl / ms / 1e9 / FP8_PEAK_TFLOPS,
+            "up_kernel_ms": ku, "up_TFLOP/s": fl / ku / 1e9, "down_kernel_ms": kd, "down_TFLOP/s": fl / kd / 1e9,
+            "backend": ctx.last_backend()}
+        wu.release()
+        wd.release()
 
-    def c1(i=0):  # QuantizeLinear, then Gemm with the DequantizeLinear fused into its epilogue
-        ctx.quantize_linear(x, L.FP32, [s_x], [0], xq)
-        ctx.i8_linear_ex(L.I8_GEMM, xq, s_x, 0, m, w8, y, L.FP32, s_y, 0, dq_scale=s_y, dq_zp=0, bias=bias,
-                         bias_kind=L.BIAS_VECTOR, bias_abs_max=20000)
+    if want("C1"):
+        # C1 INT8 linear chain: QuantizeLinear(fp32) -> Gemm INT8 (transB) -> DequantizeLinear(fp32)
+        m, k, n = 128, 1024, 1024
+        x = b.randn((m, k), 0xFEA70001)
+        s_x = float(x.abs().max()) / 127.0
+        b.gen.manual_seed(0xFEA70001 + 1)
+        wq = t.randint(-127, 128, (n, k), generator=b.gen, device="cuda", dtype=t.int8)
+        s_w = (t.rand(n, generator=b.gen, device="cuda") * 9e-3 + 1e-3).cpu().numpy()
+        bias = t.randint(-20000, 20000, (n,), generator=b.gen, device="cuda", dtype=t.int32)
+        w8 = ctx.prepare_weight(wq, L.INT8, k, n, L.LAYOUT_NK, scales=s_w, version=4)
+        xq = t.empty((m, k), dtype=t.int8, device="cuda")
+        yq = t.empty((m, n), dtype=t.int8, device="cuda")
+        y = t.empty((m, n), dtype=t.float32, device="cuda")
+        s_y = 0.05
 
-    def c1_unfused(i=0):  # the three nodes as three launches
-        ctx.quantize_linear(x, L.FP32, [s_x], [0], xq)
-        ctx.i8_linear(L.I8_GEMM, xq, s_x, 0, m, w8, yq, s_y, 0, bias=bias, bias_kind=L.BIAS_VECTOR, bias_abs_max=20000)
-        ctx.dequantize_linear(yq, [s_y], [0], y, L.FP32)
+        def c1(i=0):  # QuantizeLinear, then Gemm with the DequantizeLinear fused into its epilogue
+            ctx.quantize_linear(x, L.FP32, [s_x], [0], xq)
+            ctx.i8_linear_ex(L.I8_GEMM, xq, s_x, 0, m, w8, y, L.FP32, s_y, 0, dq_scale=s_y, dq_zp=0, bias=bias,
+                             bias_kind=L.BIAS_VECTOR, bias_abs_max=20000)
 
-    def c1_gemm(i=0):
-        ctx.i8_linear(L.I8_GEMM, xq, s_x, 0, m, w8, yq, s_y, 0, bias=bias, bias_kind=L.BIAS_VECTOR, bias_abs_max=20000)
-    ms, _ = b.graph_time([c1] * 50, 10)
-    ms_unfused, _ = b.graph_time([c1_unfused] * 50, 10)
-    kg, _ = b.kernel_time(c1_gemm, 200)
-    ops = 2.0 * m * k * n
-    res["C1_int8_linear_chain"] = {"ms_per_step": ms, "ms_per_step_three_launches": ms_unfused,
-                                   "TOPS": ops / ms / 1e9, "GB/s": 2101248 / ms / 1e6,
-                                   "gemm_kernel_ms": kg, "gemm_TOPS": ops / kg / 1e9,
-                                   "int8_frac": ops / kg / 1e9 / INT8_PEAK_TOPS}
-    w8.release()
+        def c1_unfused(i=0):  # the three nodes as three launches
+            ctx.quantize_linear(x, L.FP32, [s_x], [0], xq)
+            ctx.i8_linear(L.I8_GEMM, xq, s_x, 0, m, w8, yq, s_y, 0, bias=bias, bias_kind=L.BIAS_VECTOR, bias_abs_max=20000)
+            ctx.dequantize_linear(yq, [s_y], [0], y, L.FP32)
 
-    # C4 INT8 conv 3x3 s2 p1 [1,64,160,160] -> [1,128,80,80]
-    b.gen.manual_seed(0xFEA70004)
-    xin = t.randint(-128, 128, (1, 64, 160, 160), generator=b.gen, device="cuda", dtype=t.int8)
-    wc = t.randint(-127, 128, (128, 64, 3, 3), generator=b.gen, device="cuda", dtype=t.int8)
-    sc = (t.rand(128, generator=b.gen, device="cuda") * 9e-3 + 1e-3).cpu().numpy()
-    cb = t.randint(-20000, 20000, (128,), generator=b.gen, device="cuda", dtype=t.int32)
-    wcp = ctx.prepare_conv_weight(wc, sc, version=5)
-    yc = t.empty((1, 128, 80, 80), dtype=t.int8, device="cuda")
+        def c1_gemm(i=0):
+            ctx.i8_linear(L.I8_GEMM, xq, s_x, 0, m, w8, yq, s_y, 0, bias=bias, bias_kind=L.BIAS_VECTOR, bias_abs_max=20000)
+        ms, _ = b.graph_time([c1] * 50, 10)
+        ms_unfused, _ = b.graph_time([c1_unfused] * 50, 10)
+        kg, _ = b.kernel_time(c1_gemm, 200)
+        ops = 2.0 * m * k * n
+        res["C1_int8_linear_chain"] = {"ms_per_step": ms, "ms_per_step_three_launches": ms_unfused,
+                                       "TOPS": ops / ms / 1e9, "GB/s": 2101248 / ms / 1e6,
+                                       "gemm_kernel_ms": kg, "gemm_TOPS": ops / kg / 1e9,
+                                       "int8_frac": ops / kg / 1e9 / INT8_PEAK_TOPS}
+        w8.release()
 
-    def c4(i=0):
-        ctx.i8_conv2d(xin, L.NCHW, 0.0078125, 0, wcp, yc, 0.25, 0, stride=(2, 2), pad=(1, 1), bias=cb,
-                      bias_abs_max=20000)
-    ms, _ = b.graph_time([c4] * 50, 10)
-    kc, _ = b.kernel_time(c4, 100)
-    ops = 943718400.0
-    res["C4_int8_conv3x3s2"] = {"ms_per_step": ms, "TOPS": ops / ms / 1e9, "GB/s": 2531840 / ms / 1e6,
-                                "kernel_ms": kc, "int8_frac": ops / kc / 1e9 / INT8_PEAK_TOPS,
-                                "hbm_frac": 2531840 / kc / 1e6 / HBM_PEAK_GBS}
-    wcp.release()
+    if want("C4"):
+        # C4 INT8 conv 3x3 s2 p1 [1,64,160,160] -> [1,128,80,80]
+        b.gen.manual_seed(0xFEA70004)
+        xin = t.randint(-128, 128, (1, 64, 160, 160), generator=b.gen, device="cuda", dtype=t.int8)
+        wc = t.randint(-127, 128, (128, 64, 3, 3), generator=b.gen, device="cuda", dtype=t.int8)
+        sc = (t.rand(128, generator=b.gen, device="cuda") * 9e-3 + 1e-3).cpu().numpy()
+        cb = t.randint(-20000, 20000, (128,), generator=b.gen, device="cuda", dtype=t.int32)
+        wcp = ctx.prepare_conv_weight(wc, sc, version=5)
+        yc = t.empty((1, 128, 80, 80), dtype=t.int8, device="cuda")
 
-    # C5 BF16 LM head + argmax, V=151936 (311 MB > MALL)
-    k, v = 1024, 151936
-    wh = (b.randn((v, k), 0xFEA70005, 0.02)).to(t.bfloat16)
-    for m in (1, 8):
-        a = b.randn((m, k), 0xFEA70005 + m).to(t.bfloat16)
-        tok = t.empty(m, dtype=t.int64, device="cuda")
+        def c4(i=0):
+            ctx.i8_conv2d(xin, L.NCHW, 0.0078125, 0, wcp, yc, 0.25, 0, stride=(2, 2), pad=(1, 1), bias=cb,
+                          bias_abs_max=20000)
+        ms, _ = b.graph_time([c4] * 50, 10)
+        kc, _ = b.kernel_time(c4, 100)
+        ops = 943718400.0
+        res["C4_int8_conv3x3s2"] = {"ms_per_step": ms, "TOPS": ops / ms / 1e9, "GB/s": 2531840 / ms / 1e6,
+                                    "kernel_ms": kc, "int8_frac": ops / kc / 1e9 / INT8_PEAK_TOPS,
+                                    "hbm_frac": 2531840 / kc / 1e6 / HBM_PEAK_GBS}
+        wcp.release()
 
-        def c5(i=0, a=a, tok=tok):
-            ctx.bf16_gemv_argmax(a, wh, tok)
-        ms, _ = b.graph_time([c5] * 20, 10)
-        km, _ = b.kernel_time(c5, 50)
-        by = v * k * 2 + m * k * 2 + m * 8
-        res[f"C5_bf16_argmax_M{m}"] = {"ms_per_step": ms, "GB/s": by / ms / 1e6, "kernel_ms": km,
-                                       "hbm_frac": by / km / 1e6 / HBM_PEAK_GBS}
+    if want("C5"):
+        # C5 BF16 LM head + argmax, V=151936 (311 MB > MALL)
+        k, v = 1024, 151936
+        wh = (b.randn((v, k), 0xFEA70005, 0.02)).to(t.bfloat16)
+        for m in (1, 8):
+            a = b.randn((m, k), 0xFEA70005 + m).to(t.bfloat16)
+            tok = t.empty(m, dtype=t.int64, device="cuda")
+
+            def c5(i=0, a=a, tok=tok):
+                ctx.bf16_gemv_argmax(a, wh, tok)
+            ms, _ = b.graph_time([c5] * 20, 10)
+            km, _ = b.kernel_time(c5, 50)
+            by = v * k * 2 + m * k * 2 + m * 8
+            res[f"C5_bf16_argmax_M{m}"] = {"ms_per_step": ms, "GB/s": by / ms / 1e6, "kernel_ms": km,
+                                           "hbm_frac": by / km / 1e6 / HBM_PEAK_GBS}
+
     return res
 
 
