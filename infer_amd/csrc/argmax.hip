@@ -441,7 +441,7 @@ int launch(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k, const uint8
         int64_t mgrid = (v + 15) / 16;
         if (mgrid > cap) mgrid = cap;
 #define FHIP_ARGMAX_MFMA_CASE(SPW)                                                                                  \
-        if (spw_need <= SPW) {                                                                                      \
+        if (spw_need <= (SPW)) {                                                                                    \
             gemv_argmax_mfma_kernel<KIND, SPW><<<(unsigned)mgrid, kThreads, 0, ctx->stream>>>(a, m, k, w, v, hp,    \
                                                                                    partials, ctx->scratch, tokens); \
             ctx->last_backend = name;                                                                               \

@@ -32,11 +32,6 @@ namespace {
 // `a_vec` = 1 when k % 4 == 0 and the rows are 16-byte aligned; otherwise a per-element path runs.
 // Scales: `inv` holds 1/s when s is a power of two (x * (1/s) is then exactly x / s, both being the
 // correctly rounded value of the same real number); otherwise inv = 0 and the kernel divides.
-template <int ADT>
-struct ActGroup {
-    static constexpr int kElems = 4;
-};
-
 __device__ __forceinline__ float scale_down(float x, float s, float inv) { return inv != 0.0f ? x * inv : x / s; }
 
 template <bool E5, int ADT>
@@ -201,8 +196,8 @@ __global__ __launch_bounds__(kGemvThreads) void fp8_gemv_mfma_kernel(const void*
 // the weight stream issued right after), encoding is the hardware converter with the reference's
 // saturation fix-up, and the output type is a template parameter.
 template <int ADT>
-__device__ __forceinline__ void load_act_group(const void* __restrict__ a, int64_t k, int g, float a_inv,
-                                               uint32_t (&raw)[4], bool& live) {
+__device__ __forceinline__ void load_act_group(const void* __restrict__ a, int64_t k, int g, uint32_t (&raw)[4],
+                                               bool& live) {
     live = (int64_t)g * 4 < k;
     const int64_t e = live ? (int64_t)g * 4 : 0;
     if constexpr (ADT == 0) {
@@ -246,7 +241,7 @@ __global__ __launch_bounds__(kGemvThreads) void fp8_gemv1_kernel(const void* __r
 
     uint32_t raw[4];
     bool live;
-    load_act_group<ADT>(a, k, tid < groups ? tid : 0, a_inv, raw, live);
+    load_act_group<ADT>(a, k, tid < groups ? tid : 0, raw, live);
     live = live && tid < groups;
     uint4 wv[R];
     {
@@ -256,7 +251,7 @@ __global__ __launch_bounds__(kGemvThreads) void fp8_gemv1_kernel(const void* __r
     }
     if (tid < groups) *reinterpret_cast<uint32_t*>(xs + tid * 4) = encode_act_group<E5, ADT>(raw, a_inv, live);
     for (int g = tid + kGemvThreads; g < groups; g += kGemvThreads) {  // rows longer than 1024
-        load_act_group<ADT>(a, k, g, a_inv, raw, live);
+        load_act_group<ADT>(a, k, g, raw, live);
         *reinterpret_cast<uint32_t*>(xs + g * 4) = encode_act_group<E5, ADT>(raw, a_inv, live);
     }
     __syncthreads();
@@ -366,7 +361,6 @@ __global__ void cast_kernel(const void* __restrict__ src, int src_dtype, float s
 
 bool is_fp8(int d) { return d == FHIP_FP8E4M3 || d == FHIP_FP8E5M2; }
 bool is_castable(int d) { return d == FHIP_FP32 || d == FHIP_BF16 || d == FHIP_FP16 || is_fp8(d); }
-size_t dtype_bytes(int d) { return d == FHIP_FP32 ? 4 : (d == FHIP_BF16 || d == FHIP_FP16 ? 2 : 1); }
 
 unsigned grid_for(int64_t count, int threads) {
     int64_t blocks = (count + threads - 1) / threads;
