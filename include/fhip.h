@@ -92,6 +92,15 @@ const char* fhip_last_backend(fhip_context ctx);
 int fhip_weight_prepare(fhip_context ctx, const void* src, int dtype, int64_t k, int64_t n, int src_layout,
                         const float* scales, int64_t n_scale, const int32_t* zero_points, int64_t n_zp,
                         uint64_t version, fhip_weight* out);
+/* The same preparation from host memory, at model load (SURVEY's load-time pre-swizzle): the bytes are
+ * uploaded, re-laid out as above and keyed on (host_src, dtype, K, N, layout, version), so a loader can
+ * prepare every immutable weight once straight from the (mmapped) model file instead of at the first
+ * Prepare() from a device tensor (src/model/model_io.cc, weight_store.cc; kernel.h:160-162).  The
+ * transient device copy is freed before the call returns; the call synchronises the context's stream. */
+int fhip_weight_prepare_host(fhip_context ctx, const void* host_src, int dtype, int64_t k, int64_t n, int src_layout,
+                             const float* scales, int64_t n_scale, const int32_t* zero_points, int64_t n_zp,
+                             uint64_t version, fhip_weight* out);
+
 /* Conv2D weight [OC, IC/group, KH, KW] INT8 with per-output-channel scales (axis 0). */
 int fhip_conv_weight_prepare(fhip_context ctx, const int8_t* src, int64_t oc, int64_t icg, int64_t kh,
                              int64_t kw, int32_t group, const float* scales, int64_t n_scale,

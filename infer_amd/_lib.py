@@ -39,6 +39,7 @@ SIGNATURES = {
     "fhip_last_error": (ctypes.c_char_p, [_P]),
     "fhip_last_backend": (ctypes.c_char_p, [_P]),
     "fhip_weight_prepare": (_INT, [_P, _P, _INT, _I64, _I64, _INT, _P, _I64, _P, _I64, _U64, _PP]),
+    "fhip_weight_prepare_host": (_INT, [_P, _P, _INT, _I64, _I64, _INT, _P, _I64, _P, _I64, _U64, _PP]),
     "fhip_conv_weight_prepare": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _I32, _P, _I64, _P, _I64, _U64, _PP]),
     "fhip_weight_release": (_INT, [_P]),
     "fhip_weight_matches": (_INT, [_P, _P, _U64]),

@@ -287,15 +287,15 @@ int fhip_synchronize(fhip_context ctx) {
 const char* fhip_last_error(fhip_context ctx) { return ctx ? ctx->last_error.c_str() : "null context"; }
 const char* fhip_last_backend(fhip_context ctx) { return ctx ? ctx->last_backend : ""; }
 
-int fhip_weight_prepare(fhip_context ctx, const void* src, int dtype, int64_t k, int64_t n, int src_layout,
-                        const float* scales, int64_t n_scale, const int32_t* zero_points, int64_t n_zp,
-                        uint64_t version, fhip_weight* out) {
-    if (!ctx || !out) return FHIP_ERR_INVALID;
-    *out = nullptr;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    DeviceGuard guard(ctx->device);
+}  // extern "C"
+
+namespace {
+
+// Argument checks shared by the two linear-weight prepare entry points.
+int check_linear_weight_args(fhip_context ctx, const void* src, int dtype, int64_t k, int64_t n, int src_layout,
+                             const float* scales, int64_t n_scale, const int32_t* zero_points, int64_t n_zp) {
     if ((k == 0 || n == 0) && src_layout >= FHIP_LAYOUT_KN && src_layout <= FHIP_LAYOUT_NK)
-        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "weight_prepare: empty weight (the Common kernel handles it)");
+        return set_error(ctx, FHIP_ERR_UNSUPPORTED, "weight_prepare: empty weight (the Common kernel handles it)");
     if (!src || k <= 0 || n <= 0 || (src_layout != FHIP_LAYOUT_KN && src_layout != FHIP_LAYOUT_NK))
         return set_error(ctx, FHIP_ERR_INVALID, "weight_prepare: bad arguments");
     if (dtype != FHIP_FP8E4M3 && dtype != FHIP_FP8E5M2 && dtype != FHIP_INT8)
@@ -312,19 +312,20 @@ int fhip_weight_prepare(fhip_context ctx, const void* src, int dtype, int64_t k,
                 return set_error(ctx, FHIP_ERR_INVALID, "weight_prepare: zero point outside [-128, 127]");
     }
     if (ctx->capturing) return set_error(ctx, FHIP_ERR_STATE, "weight_prepare during capture");
-    if (fhip_weight hit = find_cached(ctx, src, dtype, k, n, src_layout, kLinearWeight, version)) {
-        hit->refs++;
-        *out = hit;
-        ctx->last_backend = "weight_cache_hit";
-        return FHIP_OK;
-    }
+    return FHIP_OK;
+}
+
+// A new prepared weight from device bytes `src`, cached under `key` (the caller's identity of the bytes).
+int make_linear_weight(fhip_context ctx, const void* src, const void* key, int dtype, int64_t k, int64_t n,
+                       int src_layout, const float* scales, int64_t n_scale, const int32_t* zero_points, int64_t n_zp,
+                       uint64_t version, fhip_weight* out) {
     auto* w = new fhip_weight_s();
     w->ctx = ctx;
     w->dtype = dtype;
     w->k = k;
     w->n = n;
     w->src_layout = src_layout;
-    w->src = src;
+    w->src = key;
     w->version = version;
     int rc = prepare_common(ctx, w, src, k, n, src_layout, scales, n_scale, zero_points, n_zp);
     if (rc != FHIP_OK) {
@@ -333,9 +334,68 @@ int fhip_weight_prepare(fhip_context ctx, const void* src, int dtype, int64_t k,
     }
     ctx->weight_bytes += w->bytes;
     ctx->weights.push_back(w);
-    ctx->last_backend = "weight_prepare";
     *out = w;
     return FHIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fhip_weight_prepare(fhip_context ctx, const void* src, int dtype, int64_t k, int64_t n, int src_layout,
+                        const float* scales, int64_t n_scale, const int32_t* zero_points, int64_t n_zp,
+                        uint64_t version, fhip_weight* out) {
+    if (!ctx || !out) return FHIP_ERR_INVALID;
+    *out = nullptr;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    DeviceGuard guard(ctx->device);
+    int rc = check_linear_weight_args(ctx, src, dtype, k, n, src_layout, scales, n_scale, zero_points, n_zp);
+    if (rc != FHIP_OK) return rc;
+    if (fhip_weight hit = find_cached(ctx, src, dtype, k, n, src_layout, kLinearWeight, version)) {
+        hit->refs++;
+        *out = hit;
+        ctx->last_backend = "weight_cache_hit";
+        return FHIP_OK;
+    }
+    rc = make_linear_weight(ctx, src, src, dtype, k, n, src_layout, scales, n_scale, zero_points, n_zp, version, out);
+    if (rc == FHIP_OK) ctx->last_backend = "weight_prepare";
+    return rc;
+}
+
+int fhip_weight_prepare_host(fhip_context ctx, const void* host_src, int dtype, int64_t k, int64_t n, int src_layout,
+                             const float* scales, int64_t n_scale, const int32_t* zero_points, int64_t n_zp,
+                             uint64_t version, fhip_weight* out) {
+    if (!ctx || !out) return FHIP_ERR_INVALID;
+    *out = nullptr;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    DeviceGuard guard(ctx->device);
+    int rc = check_linear_weight_args(ctx, host_src, dtype, k, n, src_layout, scales, n_scale, zero_points, n_zp);
+    if (rc != FHIP_OK) return rc;
+    if (fhip_weight hit = find_cached(ctx, host_src, dtype, k, n, src_layout, kLinearWeight, version)) {
+        hit->refs++;
+        *out = hit;
+        ctx->last_backend = "weight_cache_hit";
+        return FHIP_OK;
+    }
+    // Upload into a transient device copy and re-lay it out with the device path; the prepared weight is
+    // keyed on the host bytes, and the transient copy is freed before returning.
+    const size_t bytes = (size_t)k * (size_t)n;
+    void* tmp = nullptr;
+    rc = check_hip(ctx, hipMalloc(&tmp, bytes), "hipMalloc(weight upload)");
+    if (rc != FHIP_OK) return rc;
+    rc = check_hip(ctx, hipMemcpyAsync(tmp, host_src, bytes, hipMemcpyHostToDevice, ctx->stream), "weight upload");
+    if (rc == FHIP_OK)
+        rc = make_linear_weight(ctx, tmp, host_src, dtype, k, n, src_layout, scales, n_scale, zero_points, n_zp,
+                                version, out);
+    const int rs = check_hip(ctx, hipStreamSynchronize(ctx->stream), "weight upload sync");
+    (void)hipFree(tmp);
+    if (rc == FHIP_OK && rs != FHIP_OK) {
+        fhip_weight_release(*out);
+        *out = nullptr;
+        rc = rs;
+    }
+    if (rc == FHIP_OK) ctx->last_backend = "weight_prepare_host";
+    return rc;
 }
 
 int fhip_conv_weight_prepare(fhip_context ctx, const int8_t* src, int64_t oc, int64_t icg, int64_t kh, int64_t kw,

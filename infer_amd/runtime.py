@@ -117,6 +117,22 @@ class Context:
             return rc
         return Weight(self, h, w, dtype, k, n)
 
+    def prepare_weight_host(self, w, dtype, k, n, layout, scales=None, zero_points=None, version=0, check=True):
+        """w: host numpy array holding [K,N] (layout KN) or [N,K] (layout NK) bytes (e.g. a model file's
+        mmapped weight); it must stay alive while the prepared weight is cached under its address."""
+        w = np.ascontiguousarray(w)
+        sc, sp = (None, None) if scales is None else _host_array(scales, np.float32)
+        zp, zpp = (None, None) if zero_points is None else _host_array(zero_points, np.int32)
+        h = _c.c_void_p()
+        rc = self._run(self.lib.fhip_weight_prepare_host, w.ctypes.data_as(_c.c_void_p), dtype, k, n, layout, sp,
+                       0 if sc is None else sc.size, zpp, 0 if zp is None else zp.size, version, _c.byref(h),
+                       check=False)
+        if rc != 0:
+            if check:
+                self._check(rc)
+            return rc
+        return Weight(self, h, w, dtype, k, n)
+
     def prepare_conv_weight(self, w, scales, zero_points=None, group=1, version=0, check=True):
         oc, icg, kh, kw = w.shape
         sc, sp = _host_array(scales, np.float32)

@@ -70,3 +70,28 @@ def test_fp8_linear_ragged_k(ctx, dtype, m):
     ref = po.fp8_gemm(dtype, a_codes, s_in, w_nk, sw, True, s_out)
     fp8_linear_check(dtype, out.cpu().numpy(), ref, a_codes, s_in, w_nk, sw, s_out, f"ragged k m={m}")
     wt.release()
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+def test_weight_prepare_from_host_matches_device(ctx, layout):
+    """Load-time preparation from host bytes gives the same prepared weight as the device path: the
+    outputs of an FP8 linear through either are identical; the host copy is cached on its address."""
+    dtype = po.FP8E4M3
+    k, n, m = 1024, 700, 3
+    r = rng(70 + layout)
+    w_nk, sw = fp8_tensor((r.standard_normal((n, k)) * 0.02).astype(np.float32), dtype)
+    src = w_nk if layout == 1 else np.ascontiguousarray(w_nk.T)
+    a, sa = fp8_tensor(r.standard_normal((m, k)).astype(np.float32), dtype)
+    wd = ctx.prepare_weight(dev(src), dtype, k, n, layout, version=80)
+    wh = ctx.prepare_weight_host(src, dtype, k, n, layout, version=80)
+    assert ctx.last_backend() == "weight_prepare_host"
+    wh2 = ctx.prepare_weight_host(wh.source, dtype, k, n, layout, version=80)
+    assert ctx.last_backend() == "weight_cache_hit"
+    outs = []
+    for wt in (wd, wh):
+        out = torch.empty((m, n), dtype=torch.uint8, device="cuda")
+        ctx.fp8_linear(dev(a), dtype, sa, m, wt, sw, out, dtype, 0.5)
+        outs.append(out.cpu().numpy())
+    assert np.array_equal(outs[0], outs[1])
+    for wt in (wd, wh, wh2):
+        wt.release()
