@@ -4,13 +4,16 @@
 // FP8 output code, optional decode to BF16/FP32 -- src/kernel/common/gemm.cc:62-100).
 //
 // Tiling:
-//   * block tile BM x BN, 4 waves (256 threads) arranged WAVES_M x WAVES_N; K advances 64 per stage;
-//   * v_mfma_scale_f32_32x32x64_f8f6f4 with unit block scales (scale exponent 127), fp32 accumulators;
-//     lane l supplies row/column l%32 and the 32-byte K slice (l/32) of the 64-deep stage, for A and
-//     B alike, so both index the same K in every MFMA slot;
-//   * A (activations, [m][k]) and B (prepared weight, [Np][Kp]) stages live in LDS with an 80-byte row
-//     pitch: the 16 lanes of a ds_read_b128 group hit 16 distinct 4-bank groups (5*r mod 16 distinct);
-//   * two LDS stages: the global loads of stage s+1 are in flight while stage s feeds the MFMAs;
+//   * block tile BM x BN, 8 waves (512 threads) arranged WAVES_M x WAVES_N; K advances BK (64 or 128) per
+//     stage; v_mfma_scale_f32_32x32x64_f8f6f4 with unit block scales (scale exponent 127), fp32
+//     accumulators; lane l supplies row/column l%32 and the 32-byte K slice (l/32) of each 64-deep step,
+//     for A and B alike, so both index the same K in every MFMA slot;
+//   * A (activations, [m][k]) and B (prepared weight, [Np][Kp]) stages move global -> LDS with
+//     buffer_load ... lds (no VGPR round trip) through buffer resources based at the tile's first row;
+//     16-byte chunks are XOR-swizzled per row so every ds_read_b128 group of 16 lanes hits 16 distinct
+//     bank groups; a ring of STAGES buffers keeps the next stages' loads in flight;
+//   * with 128-deep stages the two 64-deep steps are software-pipelined: the fragment reads of the next
+//     step are in flight while the current step's MFMAs run;
 //   * tile order is XCD-aware: consecutive workgroups land on different XCDs (round-robin dispatch),
 //     so the tile index is re-derived to give each XCD a rectangle of tiles whose shared operand rows
 //     fit in that XCD's L2 (XcdMap);
@@ -58,19 +61,19 @@ __device__ __forceinline__ int swz(int r) { return BK == 64 ? (r >> 2) & 3 : (r 
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
-__device__ __forceinline__ void load_to_lds(const uint8_t* g, uint8_t* lds_wave_base) {
-    __builtin_amdgcn_global_load_lds(static_cast<const void*>(g), (lds_ptr)(lds_wave_base), 16, 0, 0);
-}
+// Buffer resource word 3 for raw (unstructured) byte-addressed buffers on gfx9-family parts.
+constexpr int kBufferRsrcWord3 = 0x00020000;
 
 // LDS fragment read issued as inline asm.  The compiler's wait-count pass treats every LDS read as
 // possibly aliasing the in-flight LDS-DMA stage loads and would put a vmcnt(0) in front of it, draining
 // the whole load pipeline each stage; the explicit vmcnt(N) + s_barrier above each stage already
 // orders these reads.  The matching lgkmcnt wait is lds_fence() below.
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ u32x4_t lds_read16(const uint8_t* p) {
+template <int OFF>
+__device__ __forceinline__ u32x4_t lds_read16(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds_read offset field is 16 bits");
     u32x4_t v;
-    const unsigned addr = (unsigned)(uintptr_t)(lds_ptr)(p);
-    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
     return v;
 }
 
@@ -174,6 +177,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
     constexpr int NT = 64 * WAVES_M * WAVES_N;
     using S = Stage<BM, BN, NT, BK>;
     constexpr int kSub = BK / 64;  // 64-deep MFMA steps per stage
+    static_assert(BK == 64 || BK == 128, "stage depth is 64 or 128");
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int FM = WTM / 32, FN = WTN / 32;
     static_assert(FM * 32 == WTM && FN * 32 == WTN, "wave tile must be a multiple of 32");
@@ -197,22 +201,22 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
     const int64_t m0 = (int64_t)(tile / tiles_n) * BM;
     const int64_t n0 = (int64_t)(tile % tiles_n) * BN;
 
-    // Per-thread source rows and chunks of its 16-byte loads (fixed for the whole K loop).
-    const uint8_t* src[S::kLoads];
-#pragma unroll
-    for (int i = 0; i < S::kLoads; ++i) {
-        const bool is_a = i < S::kLoadsA;
-        const int q = (is_a ? i : i - S::kLoadsA) * NT + tid;
-        const int r = q / S::kChunks;
-        const int c = (q % S::kChunks) ^ swz<BK>(r);
-        if (is_a) {
-            const int64_t row = m0 + r < m ? m0 + r : m - 1;   // rows past m are computed, never stored
-            src[i] = a + row * k + c * 16;
-        } else {
-            const int64_t row = n0 + r < np ? n0 + r : np - 1;
-            src[i] = b + row * kp + c * 16;
-        }
-    }
+    const int nk = (int)(k / BK);  // host guarantees k % BK == 0
+    // Stage loads go through buffer resources based at this tile's first row: one 32-bit offset register
+    // per 16-byte load instead of a 64-bit pointer.  A rows past m are out of the resource's range and
+    // read as zero (those rows are computed, never stored); the prepared weight is padded to np rows.
+    // The host keeps m*k and np*kp below 2^31.
+    const __amdgpu_buffer_rsrc_t rsrc_a =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(a + m0 * k), 0, (int)((m - m0) * k), kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rsrc_b =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(b + n0 * kp), 0, (int)((np - n0) * kp), kBufferRsrcWord3);
+    // Slot i of a thread's loads covers row r0 + i * kRowsPerPass, same chunk (the swizzle repeats every 16
+    // rows), so one base offset per operand plus a uniform per-slot, per-stage term addresses every load.
+    static_assert(S::kRowsPerPass % 16 == 0, "slot rows must keep the swizzle phase");
+    const int r0 = tid / S::kChunks;
+    const int c0s = (tid % S::kChunks) ^ swz<BK>(r0);
+    const uint32_t voff_a = (uint32_t)(r0 * k + c0s * 16);
+    const uint32_t voff_b = (uint32_t)(r0 * kp + c0s * 16);
     auto issue = [&](int kt) {
         uint8_t* st = smem + (kt % STAGES) * S::kBytes;
 #pragma unroll
@@ -220,7 +224,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
             const bool is_a = i < S::kLoadsA;
             const int slot = is_a ? i : i - S::kLoadsA;
             uint8_t* dst = st + (is_a ? 0 : S::kA) + (slot * NT + wave * 64) * 16;
-            load_to_lds(src[i] + (int64_t)kt * BK, dst);
+            // the uniform term varies with kt, so the per-slot sums are not hoisted into live registers
+            const uint32_t u = (uint32_t)(slot * S::kRowsPerPass * (is_a ? k : kp) + (int64_t)kt * BK);
+            // a stage past the last is out of the resource's range (operands are below 2^31 bytes)
+            const uint32_t off = kt < nk ? (is_a ? voff_a : voff_b) + u : 0x80000000u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(is_a ? rsrc_a : rsrc_b, (lds_ptr)dst, 16, off, 0, 0, 0);
         }
     };
 
@@ -232,62 +240,108 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    const int nk = (int)(k / BK);  // host guarantees k % BK == 0
-#pragma unroll
-    for (int s0 = 0; s0 < STAGES - 1; ++s0)
-        if (s0 < nk) issue(s0);
-
     const int frag_row = lane & 31;
     const int frag_c = (lane >> 5) * 2;
-    for (int kt = 0; kt < nk; ++kt) {
-        // stages issued after kt: min(STAGES - 2, nk - 1 - kt); wait until at most that many are in flight
+    // Fragment reads of 64-deep step u of the stage at byte offset `st` into fa/fb.  The swizzle of a
+    // fragment row depends only on frag_row (wave and fragment row offsets are multiples of 32), so every
+    // read is one of four per-thread column offsets plus a per-thread row base, a uniform stage offset
+    // and a compile-time immediate; no per-fragment address registers stay live across the loop.
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr)smem;
+    const uint32_t row_a = lds0 + (uint32_t)((wm * WTM + frag_row) * BK);
+    const uint32_t row_b = lds0 + (uint32_t)(S::kA + (wn * WTN + frag_row) * BK);
+    const uint32_t col0 = (uint32_t)((frag_c ^ swz<BK>(frag_row)) << 4);
+    const uint32_t col1 = (uint32_t)(((frag_c + 1) ^ swz<BK>(frag_row)) << 4);
+    auto read_frags = [&](uint32_t st, int u, u32x4_t (&fa)[FM][2], u32x4_t (&fb)[FN][2]) {
+        const uint32_t cu = (uint32_t)u * 64u;  // chunk index + 4u: frag_c + 1 < 4, so XOR with 4 adds 4u
+        const uint32_t a0 = row_a + st + (col0 ^ cu), a1 = row_a + st + (col1 ^ cu);
+        const uint32_t b0 = row_b + st + (col0 ^ cu), b1 = row_b + st + (col1 ^ cu);
+        static_for<FM>([&](auto ii) {
+            constexpr int i = decltype(ii)::value;
+            fa[i][0] = lds_read16<i * 32 * BK>(a0);
+            fa[i][1] = lds_read16<i * 32 * BK>(a1);
+        });
+        static_for<FN>([&](auto jj) {
+            constexpr int j = decltype(jj)::value;
+            fb[j][0] = lds_read16<j * 32 * BK>(b0);
+            fb[j][1] = lds_read16<j * 32 * BK>(b1);
+        });
+    };
+    auto mfmas = [&](const u32x4_t (&fa)[FM][2], const u32x4_t (&fb)[FN][2]) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const v8i av = v8i{(int)fa[i][0].x, (int)fa[i][0].y, (int)fa[i][0].z, (int)fa[i][0].w,
+                                   (int)fa[i][1].x, (int)fa[i][1].y, (int)fa[i][1].z, (int)fa[i][1].w};
+                const v8i bv = v8i{(int)fb[j][0].x, (int)fb[j][0].y, (int)fb[j][0].z, (int)fb[j][0].w,
+                                   (int)fb[j][1].x, (int)fb[j][1].y, (int)fb[j][1].z, (int)fb[j][1].w};
+                // weight fragment as the row operand: each 32x32 block is computed transposed
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[i][j], fmt, fmt, 0, 127, 0, 127);
+            }
+    };
+    // Wait until at most min(STAGES - 2, nk - 1 - kt) stages issued after stage kt are still in flight.
+    auto wait_stage = [&](int kt) {
         const int ahead = nk - 1 - kt;
         if (STAGES >= 4 && ahead >= 2) wait_vmcnt<2 * S::kLoads>();
         else if (STAGES >= 3 && ahead >= 1) wait_vmcnt<S::kLoads>();
         else wait_vmcnt<0>();
-        // Plain s_barrier: the explicit vmcnt wait above already covers this wave's stage loads, and a
-        // __syncthreads() fence would also wait for the loads of the stages still in flight.
+    };
+
+    if constexpr (kSub == 2) {
+        // Software pipeline over the two 64-deep steps of each stage: the fragment reads of the next step
+        // (of this stage, or the first step of the next stage, after its barrier) are in flight while the
+        // MFMAs of the current step run.  A stage's buffer is refilled only after the barrier that follows
+        // every wave's last read of it.
+        // The loop body has no branch (a branch lets the compiler sink the first step's MFMAs below it,
+        // keeping two copies of the f0 fragments alive): stages past the last are issued as out-of-range
+        // loads, which move nothing from memory and write zeros into a buffer nobody reads again, so
+        // exactly STAGES - 2 stages are in flight behind the one waited for.
+        u32x4_t f0a[FM][2], f0b[FN][2], f1a[FM][2], f1b[FN][2];
+        for (int s0 = 0; s0 < STAGES - 1; ++s0) issue(s0);
+        wait_vmcnt<(STAGES - 2) * S::kLoads>();
         __builtin_amdgcn_s_barrier();
-        if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1);
-        const uint8_t* sa = smem + (kt % STAGES) * S::kBytes;
-        const uint8_t* sb = sa + S::kA;
-        u32x4_t fa[kSub][FM][2], fb[kSub][FN][2];
-#pragma unroll
-        for (int u = 0; u < kSub; ++u) {
-            const int c0 = u * 4 + frag_c;
-#pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                const int r = wm * WTM + i * 32 + frag_row;
-                const uint8_t* row = sa + r * BK;
-                fa[u][i][0] = lds_read16(row + ((c0 ^ swz<BK>(r)) << 4));
-                fa[u][i][1] = lds_read16(row + (((c0 + 1) ^ swz<BK>(r)) << 4));
-            }
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                const int r = wn * WTN + j * 32 + frag_row;
-                const uint8_t* row = sb + r * BK;
-                fb[u][j][0] = lds_read16(row + ((c0 ^ swz<BK>(r)) << 4));
-                fb[u][j][1] = lds_read16(row + (((c0 + 1) ^ swz<BK>(r)) << 4));
-            }
+        issue(STAGES - 1);
+        read_frags(0u, 0, f0a, f0b);
+        lds_fence<FM, FN>(f0a, f0b);
+        for (int kt = 0; kt < nk - 1; ++kt) {
+            read_frags((uint32_t)((kt % STAGES) * S::kBytes), 1, f1a, f1b);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(f0a, f0b);
+            __builtin_amdgcn_sched_barrier(0);
+            lds_fence<FM, FN>(f1a, f1b);
+            wait_vmcnt<(STAGES - 2) * S::kLoads>();
+            __builtin_amdgcn_s_barrier();
+            issue(kt + STAGES);
+            read_frags((uint32_t)(((kt + 1) % STAGES) * S::kBytes), 0, f0a, f0b);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(f1a, f1b);
+            __builtin_amdgcn_sched_barrier(0);
+            lds_fence<FM, FN>(f0a, f0b);
         }
-        // Wait for the fragment reads; every fragment register is an operand, so no MFMA that uses one
-        // can be scheduled above the wait.
+        read_frags((uint32_t)(((nk - 1) % STAGES) * S::kBytes), 1, f1a, f1b);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(f0a, f0b);
+        __builtin_amdgcn_sched_barrier(0);
+        lds_fence<FM, FN>(f1a, f1b);
+        mfmas(f1a, f1b);
+        wait_vmcnt<0>();  // the trailing out-of-range loads still write LDS, which the epilogue reuses
+    } else {
 #pragma unroll
-        for (int u = 0; u < kSub; ++u) lds_fence<FM, FN>(fa[u], fb[u]);
-#pragma unroll
-        for (int u = 0; u < kSub; ++u)
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j) {
-                    const v8i av = v8i{(int)fa[u][i][0].x, (int)fa[u][i][0].y, (int)fa[u][i][0].z, (int)fa[u][i][0].w,
-                                       (int)fa[u][i][1].x, (int)fa[u][i][1].y, (int)fa[u][i][1].z, (int)fa[u][i][1].w};
-                    const v8i bv = v8i{(int)fb[u][j][0].x, (int)fb[u][j][0].y, (int)fb[u][j][0].z, (int)fb[u][j][0].w,
-                                       (int)fb[u][j][1].x, (int)fb[u][j][1].y, (int)fb[u][j][1].z, (int)fb[u][j][1].w};
-                    // weight fragment as the row operand: each 32x32 block is computed transposed
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[i][j], fmt, fmt, 0, 127, 0,
-                                                                                 127);
-                }
+        for (int s0 = 0; s0 < STAGES - 1; ++s0)
+            if (s0 < nk) issue(s0);
+        for (int kt = 0; kt < nk; ++kt) {
+            wait_stage(kt);
+            // Plain s_barrier: the explicit vmcnt wait above already covers this wave's stage loads, and a
+            // __syncthreads() fence would also wait for the loads of the stages still in flight.
+            __builtin_amdgcn_s_barrier();
+            if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1);
+            u32x4_t fa[FM][2], fb[FN][2];
+            read_frags((uint32_t)((kt % STAGES) * S::kBytes), 0, fa, fb);
+            // Wait for the fragment reads; every fragment register is an operand, so no MFMA that uses
+            // one can be scheduled above the wait.
+            lds_fence<FM, FN>(fa, fb);
+            mfmas(fa, fb);
+        }
     }
     __syncthreads();
 
@@ -355,6 +409,8 @@ int launch_tile(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, cons
     const int tiles_m = (int)((m + BM - 1) / BM), tiles_n = (int)((w->n + BN - 1) / BN);
     const int tiles = tiles_m * tiles_n;
     const int grid = tiles;  // the kernel remaps tiles XCD-wise
+    if (m * k64 >= (int64_t(1) << 31) || np * kp >= (int64_t(1) << 31))
+        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "fp8 gemm: operands of 2 GiB or more");
     XcdMap xm{1, 0, 1};
     {
         const int splits[4][2] = {{8, 1}, {4, 2}, {2, 4}, {1, 8}};

@@ -134,13 +134,14 @@ def test_fp8_gemv_fused_bf16_io(ctx, dtype, m):
 
 
 @pytest.mark.parametrize("dtype", FP8)
-@pytest.mark.parametrize("shape", [(256, 1024, 512), (100, 384, 200), (200, 320, 300), (4096, 1024, 3584)])
+@pytest.mark.parametrize("shape", [(256, 1024, 512), (100, 384, 200), (200, 320, 300), (300, 128, 520),
+                                   (4096, 1024, 3584), (4000, 1152, 3584)])
 def test_fp8_mfma_gemm_matches_oracle(ctx, dtype, shape):
     m, k, n = shape
     a, sa, w_nk, w_src, sw, s_out = _linear_case(SEEDS[3] + m, dtype, m, k, n, 1)
     if m * n > 1 << 21:
-        # full-size case: check a seeded subset of rows against the oracle
-        rows = np.sort(rng(7).choice(m, 96, replace=False))
+        # full-size case: a seeded subset of rows plus the last rows (a partial row tile when m % 256 != 0)
+        rows = np.union1d(rng(7).choice(m, 96, replace=False), np.arange(m - 8, m))
     else:
         rows = np.arange(m)
     wt = ctx.prepare_weight(dev(w_src), dtype, k, n, 1, version=3)
