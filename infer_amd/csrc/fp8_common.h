@@ -105,20 +105,28 @@ __device__ __forceinline__ float decode_code(uint32_t code) {
     return (d.x != d.x) ? __uint_as_float(0x7fc00000u) : d.x;  // the reference decodes NaN codes to +qNaN
 }
 
-// Four values -> four FP8 codes packed little-endian: hardware converter for finite in-range values,
-// reference saturated / special codes otherwise (NaN fails every comparison and takes the fix-up).
+// Four values -> four FP8 codes packed little-endian.  encode4_hw: the hardware converter's codes, which
+// are the reference's for finite in-range values, and whether all four are such values (NaN fails every
+// comparison).  encode4: the reference's codes, with saturated / special codes patched in.
 template <bool E5>
-__device__ __forceinline__ uint32_t encode4(const float (&q)[4]) {
+__device__ __forceinline__ uint32_t encode4_hw(const float (&q)[4], bool& in_range) {
     int pk = E5 ? __builtin_amdgcn_cvt_pk_bf8_f32(q[0], q[1], 0, false) : __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
     pk = E5 ? __builtin_amdgcn_cvt_pk_bf8_f32(q[2], q[3], pk, true) : __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], pk, true);
     const float maxf = E5 ? 57344.0f : 448.0f;
-    uint32_t packed = (uint32_t)pk;
-    const bool in_range = __builtin_fabsf(q[0]) <= maxf && __builtin_fabsf(q[1]) <= maxf &&
-                          __builtin_fabsf(q[2]) <= maxf && __builtin_fabsf(q[3]) <= maxf;
+    in_range = __builtin_fabsf(q[0]) <= maxf && __builtin_fabsf(q[1]) <= maxf && __builtin_fabsf(q[2]) <= maxf &&
+               __builtin_fabsf(q[3]) <= maxf;
+    return (uint32_t)pk;
+}
+
+template <bool E5>
+__device__ __forceinline__ uint32_t encode4(const float (&q)[4]) {
+    bool in_range;
+    const uint32_t pk = encode4_hw<E5>(q, in_range);
+    uint32_t packed = pk;
     if (__builtin_expect(!in_range, 0)) {
         packed = 0;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) packed |= fixup_code<E5>(q[t], ((uint32_t)pk >> (8 * t)) & 0xffu) << (8 * t);
+        for (int t = 0; t < 4; ++t) packed |= fixup_code<E5>(q[t], (pk >> (8 * t)) & 0xffu) << (8 * t);
     }
     return packed;
 }

@@ -5,7 +5,7 @@
 //
 // Tiling:
 //   * block tile BM x BN, 8 waves (512 threads) arranged WAVES_M x WAVES_N; K advances BK (64 or 128) per
-//     stage; v_mfma_scale_f32_32x32x64_f8f6f4 with unit block scales (scale exponent 127), fp32
+//     stage; v_mfma_scale_f32_32x32x64_f8f6f4 (block scale 1, or a folded power-of-two output factor), fp32
 //     accumulators; lane l supplies row/column l%32 and the 32-byte K slice (l/32) of each 64-deep step,
 //     for A and B alike, so both index the same K in every MFMA slot;
 //   * A (activations, [m][k]) and B (prepared weight, [Np][Kp]) stages move global -> LDS with
@@ -20,6 +20,7 @@
 //   * epilogue: accumulators -> output bits -> LDS tile -> coalesced 16-byte global stores.
 #include "fp8_common.h"
 
+#include <cmath>
 #include <utility>
 
 namespace {
@@ -97,20 +98,43 @@ __device__ __forceinline__ void wait_vmcnt() {
 // suite); values beyond the largest finite code are replaced with the reference's saturated / special
 // codes by selects: finite overflow -> max finite, Inf -> 0x7e (e4m3) / 0x7c (e5m2), NaN -> 0x7f / 0x7d,
 // each with the value's sign (include/util/fp8.h:66-211).
-// y / out_scale for one accumulator.  Without a bias the whole chain acc*ab_scale*alpha/out_scale is one
-// multiply by a precombined factor when out_scale is a power of two (`mul`); with a bias it follows the
-// reference's order: alpha*sum + beta*bias, then the division by out_scale (gemm.cc:87-98).
-template <bool E5, bool POW2, bool BIAS>
+// Scale modes of the epilogue (host-selected):
+//   kScaleGeneral: any out_scale; the reference's order and its division (gemm.cc:87-98);
+//   kScalePow2:    out_scale a power of two; without a bias acc*ab_scale*alpha/out_scale is one multiply
+//                  by the precombined factor `mul`; with a bias the reference's order, then * 1/out_scale;
+//   kScaleFolded:  no bias and `mul` = 2^e with |e| <= 64: the factor rides on the MFMA's block-scale
+//                  operand, so the accumulators already hold y / out_scale.  Scaling by 2^e is exact for
+//                  every product and partial sum of FP8 values in that range (|e| <= 64 keeps them normal
+//                  and finite in fp32), so the result equals acc * mul.
+constexpr int kScaleGeneral = 0, kScalePow2 = 1, kScaleFolded = 2;
+
+template <bool E5, int SM, bool BIAS>
 __device__ __forceinline__ float scaled(const Fp8Epilogue& ep, float mul, float acc, int64_t row, int64_t col) {
-    if constexpr (!BIAS) {
-        if constexpr (POW2) return acc * mul;
+    if constexpr (SM == kScaleFolded) {
+        return acc;
+    } else if constexpr (!BIAS) {
+        if constexpr (SM == kScalePow2) return acc * mul;
         return (acc * ep.ab_scale * ep.alpha) / ep.out_scale;
     } else {
         float y = acc * ep.ab_scale * ep.alpha;
         const uint8_t bc = ep.bias[ep.bias_kind == FHIP_BIAS_VECTOR ? col : row * ep.n + col];
         y += ep.beta * (fhip::fp8_decode(bc, E5) * ep.bias_scale);
-        return POW2 ? y * ep.out_inv : y / ep.out_scale;
+        return SM == kScalePow2 ? y * ep.out_inv : y / ep.out_scale;
     }
+}
+
+// Hardware FP8 codes of four values, and a running flag whose bit 7 of some byte ends up set when a code
+// is a special one: e4m3 0x7f (NaN, which the non-saturating converter also gives for |x| >= 464 and
+// Inf) or e5m2 exponent 11111 (Inf for |x| >= 61440, NaN).  Values the reference saturates but that
+// round below those thresholds (448 < |x| < 464, 57344 < |x| < 61440) already get the max-finite code.
+// Masked bytes are at most 0x7f / 0x7c, so adding 1 / 4 carries into bit 7 only from an all-ones field.
+template <bool E5>
+__device__ __forceinline__ uint32_t encode4_flag(const float (&q)[4], uint32_t& flag) {
+    int pk = E5 ? __builtin_amdgcn_cvt_pk_bf8_f32(q[0], q[1], 0, false) : __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+    pk = E5 ? __builtin_amdgcn_cvt_pk_bf8_f32(q[2], q[3], pk, true) : __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], pk, true);
+    constexpr uint32_t kMask = E5 ? 0x7c7c7c7cu : 0x7f7f7f7fu, kOne = E5 ? 0x04040404u : 0x01010101u;
+    flag |= ((uint32_t)pk & kMask) + kOne;
+    return (uint32_t)pk;
 }
 
 // Output bits of four consecutive columns (col..col+3) of one row, packed little-endian: four FP8 codes
@@ -119,16 +143,18 @@ __device__ __forceinline__ float scaled(const Fp8Epilogue& ep, float mul, float 
 // such input by the GPU test suite); beyond the largest finite code the reference's saturated and
 // special codes are selected instead: finite overflow -> max finite, Inf -> 0x7e (e4m3) / 0x7c (e5m2),
 // NaN -> 0x7f / 0x7d, each with the value's sign (include/util/fp8.h:66-211).
-template <bool E5, bool POW2, bool BIAS, int OUT_BYTES>
+// FIX = false: hardware codes only, with `flag` marking special codes (encode4_flag; the caller then
+// redoes the tile with FIX = true, so the patch-up code stays out of the hot path).
+template <bool E5, int SM, bool BIAS, int OUT_BYTES, bool FIX>
 __device__ __forceinline__ void fast_value4(const Fp8Epilogue& ep, float mul, const float (&acc)[4], int64_t row,
-                                            int64_t col, uint32_t (&out)[OUT_BYTES]) {
+                                            int64_t col, uint32_t (&out)[OUT_BYTES], uint32_t& flag) {
     float q[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) q[t] = scaled<E5, POW2, BIAS>(ep, mul, acc[t], row, col + t);
-    const uint32_t packed = encode4<E5>(q);
+    for (int t = 0; t < 4; ++t) q[t] = scaled<E5, SM, BIAS>(ep, mul, acc[t], row, col + t);
+    const uint32_t packed = FIX ? encode4<E5>(q) : encode4_flag<E5>(q, flag);
     if constexpr (OUT_BYTES == 1) {
         out[0] = packed;
-    } else if constexpr (POW2) {
+    } else if constexpr (SM != kScaleGeneral) {
         // out_scale is a power of two in [2^-100, 2^100] (host-checked): Dec(code) * out_scale is exact and
         // normal in fp32, so its BF16 form is the upper half of its bits (no rounding happens).  The
         // reference decodes every NaN code to +qNaN; the hardware keeps the sign, so NaN is replaced.
@@ -170,10 +196,10 @@ struct XcdMap {
     int gn, rm, rn;  // rm == 0: no rectangle split
 };
 
-template <bool E5, int BM, int BN, int WAVES_M, int WAVES_N, int OUT_BYTES, bool POW2, int BK, int STAGES>
+template <bool E5, int BM, int BN, int WAVES_M, int WAVES_N, int OUT_BYTES, int SM, int BK, int STAGES>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const uint8_t* __restrict__ a, int64_t m, int64_t k,
                                                        const uint8_t* __restrict__ b, int64_t kp, int64_t np,
-                                                       int tiles_n, int tiles_total, XcdMap xm, Fp8Epilogue ep) {
+                                                       int tiles_n, int tiles_total, XcdMap xm, int mfma_scale, Fp8Epilogue ep) {
     constexpr int NT = 64 * WAVES_M * WAVES_N;
     using S = Stage<BM, BN, NT, BK>;
     constexpr int kSub = BK / 64;  // 64-deep MFMA steps per stage
@@ -276,7 +302,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
                 const v8i bv = v8i{(int)fb[j][0].x, (int)fb[j][0].y, (int)fb[j][0].z, (int)fb[j][0].w,
                                    (int)fb[j][1].x, (int)fb[j][1].y, (int)fb[j][1].z, (int)fb[j][1].w};
                 // weight fragment as the row operand: each 32x32 block is computed transposed
-                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[i][j], fmt, fmt, 0, 127, 0, 127);
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[i][j], fmt, fmt, 0, mfma_scale, 0, 127);
             }
     };
     // Wait until at most min(STAGES - 2, nk - 1 - kt) stages issued after stage kt are still in flight.
@@ -354,8 +380,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
     const int row_in = lane & 31;
     const int col_q = (lane >> 5) * 4;
     const float mul = ep.ab_scale * ep.alpha * ep.out_inv;
-    auto epilogue = [&](auto bias_tag) {
-        constexpr bool BIAS = decltype(bias_tag)::value;
+    auto stage_tile = [&](auto bias_tag, auto fix_tag) __attribute__((always_inline)) {
+        constexpr bool BIAS = decltype(bias_tag)::value, FIX = decltype(fix_tag)::value;
+        uint32_t flag = 0;
         static_for<FM * FN>([&](auto ij) {
             constexpr int i = decltype(ij)::value / FN, j = decltype(ij)::value % FN;
             static_for<4>([&](auto gg) {
@@ -364,13 +391,26 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
                 const int c = wn * WTN + j * 32 + g * 8 + col_q;
                 const float v4[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
                 uint32_t packed[OUT_BYTES];
-                fast_value4<E5, POW2, BIAS, OUT_BYTES>(ep, mul, v4, m0 + r, n0 + c, packed);
+                fast_value4<E5, SM, BIAS, OUT_BYTES, FIX>(ep, mul, v4, m0 + r, n0 + c, packed, flag);
                 uint8_t* dst = so + r * kOutPitch + c * OUT_BYTES;
                 if constexpr (OUT_BYTES == 1) *reinterpret_cast<uint32_t*>(dst) = packed[0];
                 else if constexpr (OUT_BYTES == 2) *reinterpret_cast<uint2*>(dst) = make_uint2(packed[0], packed[1]);
                 else *reinterpret_cast<uint4*>(dst) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
             });
         });
+        return (flag & 0x80808080u) != 0;
+    };
+    // Hot pass with the hardware codes; a lane that met a value beyond the largest finite code (or
+    // Inf/NaN) rewrites its whole share with the reference's codes in a separate, cold pass.
+    auto epilogue = [&](auto bias_tag) {
+        if (__builtin_expect(stage_tile(bias_tag, std::false_type{}), 0)) {
+            // opaque to the optimiser, so the hot pass's intermediate values are not kept alive for reuse here
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) asm volatile("" : "+v"(acc[i][j]));
+            stage_tile(bias_tag, std::true_type{});
+        }
     };
     if (ep.bias_kind != FHIP_BIAS_NONE) epilogue(std::true_type{});
     else epilogue(std::false_type{});
@@ -428,19 +468,36 @@ int launch_tile(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, cons
     const uint8_t* wd = static_cast<const uint8_t*>(w->data);
     // power-of-two output scale in a range where decoded outputs stay exact normal fp32 values
     const bool pow2 = ep.out_inv != 0.0f && ep.out_scale >= 0x1p-100f && ep.out_scale <= 0x1p100f;
-#define FHIP_GEMM_LAUNCH(OB, P)                                                                                     \
-    fp8_gemm_kernel<E5, BM, BN, WAVES_M, WAVES_N, OB, P, BK, STAGES><<<grid, 64 * WAVES_M * WAVES_N,                             \
+    int sm = pow2 ? kScalePow2 : kScaleGeneral;
+    int mfma_scale = 127;  // E8M0 block scale 2^(s - 127)
+    if (pow2 && ep.bias_kind == FHIP_BIAS_NONE) {
+        const float mul = ep.ab_scale * ep.alpha * ep.out_inv;
+        int e = 0;
+        if (std::isfinite(mul) && std::frexp(mul, &e) == 0.5f && e - 1 >= -64 && e - 1 <= 64) {
+            sm = kScaleFolded;
+            mfma_scale = 127 + (e - 1);
+        }
+    }
+#define FHIP_GEMM_LAUNCH(OB, SMV)                                                                                   \
+    fp8_gemm_kernel<E5, BM, BN, WAVES_M, WAVES_N, OB, SMV, BK, STAGES><<<grid, 64 * WAVES_M * WAVES_N,                           \
                                                           lds_bytes<BM, BN, 64 * WAVES_M * WAVES_N, OB, BK, STAGES>(), ctx->stream>>>( \
-        a, m, k64, wd, kp, np, tiles_n, tiles, xm, ep)
+        a, m, k64, wd, kp, np, tiles_n, tiles, xm, mfma_scale, ep)
+#define FHIP_GEMM_LAUNCH_SM(OB)                                                                                     \
+    do {                                                                                                            \
+        if (sm == kScaleFolded) FHIP_GEMM_LAUNCH(OB, kScaleFolded);                                                 \
+        else if (sm == kScalePow2) FHIP_GEMM_LAUNCH(OB, kScalePow2);                                                \
+        else FHIP_GEMM_LAUNCH(OB, kScaleGeneral);                                                                   \
+    } while (0)
     if (ep.out_dtype == FHIP_FP32) {
         if (lds_bytes<BM, BN, 64 * WAVES_M * WAVES_N, 4, BK, STAGES>() > 160 * 1024)
             return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "fp8 gemm: fp32 output tile too large");
-        if (pow2) FHIP_GEMM_LAUNCH(4, true); else FHIP_GEMM_LAUNCH(4, false);
+        FHIP_GEMM_LAUNCH_SM(4);
     } else if (ep.out_dtype == FHIP_BF16) {
-        if (pow2) FHIP_GEMM_LAUNCH(2, true); else FHIP_GEMM_LAUNCH(2, false);
+        FHIP_GEMM_LAUNCH_SM(2);
     } else {
-        if (pow2) FHIP_GEMM_LAUNCH(1, true); else FHIP_GEMM_LAUNCH(1, false);
+        FHIP_GEMM_LAUNCH_SM(1);
     }
+#undef FHIP_GEMM_LAUNCH_SM
 #undef FHIP_GEMM_LAUNCH
     ctx->last_backend = name;
     FHIP_CHECK_LAUNCH(ctx, "fp8_gemm_kernel");

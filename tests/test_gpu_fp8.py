@@ -246,3 +246,62 @@ def test_fp8_linear_rejects_bad_scale(ctx):
     rc = ctx.fp8_linear(dev(a), dtype, sa, 2, wt, sw, out, dtype, 0.0, check=False)
     assert rc == -1
     wt.release()
+
+
+def _special_case(dtype, m, k, n, seed):
+    """Activations with NaN / Inf codes planted in a few rows, everything else N(0,1); returns the codes,
+    the planted rows and the usual scales."""
+    a, sa, w_nk, w_src, sw, s_out = _linear_case(seed, dtype, m, k, n, 1)
+    a = a.copy()
+    nan = 0x7F if dtype == po.FP8E4M3 else 0x7E
+    plants = {3: [nan], 7: [nan | 0x80]}
+    if dtype == po.FP8E5M2:
+        plants[11] = [0x7C]        # +Inf: Inf * w gives +-Inf per column, NaN where w == 0
+        plants[13] = [0xFC, 0x7C]  # -Inf and +Inf in one row: NaN
+    for r, codes in plants.items():
+        for j, c in enumerate(codes):
+            a[r, 5 + 17 * j] = c
+    return a, sa, w_nk, w_src, sw, s_out, sorted(plants)
+
+
+@pytest.mark.parametrize("dtype", FP8)
+@pytest.mark.parametrize("shape", [(256, 512, 384), (4096, 256, 3584)])
+@pytest.mark.parametrize("mode", ["folded", "pow2_alpha", "general"])
+def test_fp8_gemm_special_values_and_saturation(ctx, dtype, shape, mode):
+    """NaN/Inf inputs and outputs far beyond the largest finite code, through each epilogue scale mode:
+    a power-of-two output factor folded into the MFMA block scale, a power-of-two output scale with a
+    non-power-of-two alpha, and a non-power-of-two output scale.  The output scale is 1/16 of the one
+    that fits the sums, so most large outputs saturate; special and saturated codes must match exactly."""
+    m, k, n = shape
+    a, sa, w_nk, w_src, sw, s_fit, special_rows = _special_case(dtype, m, k, n, SEEDS[3] + 7 * m + k)
+    s_out = s_fit / 16 if mode != "general" else s_fit / 16 * 1.37
+    alpha = 0.3 if mode == "pow2_alpha" else 1.0
+    rows = np.union1d(np.arange(16), rng(9).choice(m, 48, replace=False)) if m > 1024 else np.arange(m)
+    wt = ctx.prepare_weight(dev(w_src), dtype, k, n, 1, version=5)
+    out = torch.empty((m, n), dtype=torch.uint8, device="cuda")
+    ctx.fp8_linear(dev(a), dtype, sa, m, wt, sw, out, dtype, s_out, alpha=alpha)
+    assert ctx.last_backend().startswith("fp8_mfma_gemm")
+    got = host(out)[rows]
+    ref = po.fp8_gemm(dtype, a[rows], sa, w_nk, sw, True, s_out, alpha=alpha)
+    dec = po.fp8_decode_table(dtype)
+    maxf = np.nanmax(np.abs(dec[np.isfinite(dec)]))
+    ref_val = dec[ref]
+    must_match = ~np.isfinite(ref_val) | np.isnan(ref_val) | (np.abs(ref_val) >= maxf)
+    sums = po.fp8_sums(dtype, a[rows], sa, w_nk, sw, True) * alpha / s_out
+    must_match &= ~np.isfinite(sums) | (np.abs(sums) >= 2 * maxf)  # far past the top code: no rounding doubt
+    assert must_match.sum() > 100
+    # a NaN's sign comes from the arithmetic that made it (x86 and the GPU differ for Inf - Inf), so NaN
+    # outputs are compared as NaN; Inf and saturated codes, with their signs, are compared exactly
+    ref_nan = np.isnan(ref_val)
+    assert np.all(np.isnan(dec[got][ref_nan]))
+    mism = np.nonzero(must_match & ~ref_nan & (got != ref))
+    assert mism[0].size == 0, f"{mism[0].size} special/saturated mismatches, first got {got[mism][:8]} ref {ref[mism][:8]}"
+    for r in special_rows:
+        i = int(np.nonzero(rows == r)[0][0])
+        assert np.all(~np.isfinite(dec[got[i]]) | (np.abs(dec[got[i]]) >= maxf))
+    keep = ~must_match
+    ordinary = np.setdiff1d(np.arange(rows.size), [int(np.nonzero(rows == r)[0][0]) for r in special_rows])
+    fp8_linear_check(dtype, np.where(keep, got, 0)[ordinary].astype(np.uint8),
+                     np.where(keep, ref, 0)[ordinary].astype(np.uint8), a[rows][ordinary], sa, w_nk, sw, s_out,
+                     f"special {shape} {mode}")
+    wt.release()
