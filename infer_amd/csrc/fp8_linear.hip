@@ -47,7 +47,7 @@ __device__ __forceinline__ void stage_activations(const void* __restrict__ a, in
                                                   int64_t m, int64_t k, int64_t kp, int mt, uint8_t* xs, int tid,
                                                   F&& after_first_loads) {
     bool first = true;
-    constexpr int kBatch = MT == 1 ? 1 : 4;  // one row of up to 1024 codes is one group per thread
+    constexpr int kBatch = MT == 1 ? 1 : (MT <= 4 ? 4 : 16);  // MT rows of up to 1024 codes: one batch
     constexpr int esz = ADT == 0 ? 1 : (ADT == 1 ? 2 : 4);
     const int64_t groups = (int64_t)mt * kp / 4;
     const int64_t gpr = kp / 4;  // groups per row
@@ -130,7 +130,7 @@ __device__ __forceinline__ void stage_activations(const void* __restrict__ a, in
 // right after the activation loads, so the weight stream and the staging overlap.
 constexpr int kGemvUnroll = 4;  // steps per wave whose weight loads are in flight together
 
-template <bool E5, int ADT>
+template <bool E5, int ADT, int MT>
 __global__ __launch_bounds__(kGemvThreads) void fp8_gemv_mfma_kernel(const void* __restrict__ a, int a_vec,
                                                                       float a_scale, float a_inv, int64_t m, int64_t k,
                                                                       const uint8_t* __restrict__ w, int64_t kp,
@@ -155,7 +155,7 @@ __global__ __launch_bounds__(kGemvThreads) void fp8_gemv_mfma_kernel(const void*
             wb[u][1] = load_stream16(p + 16);
         }
     };
-    stage_activations<E5, ADT, 16>(a, a_vec, a_scale, a_inv, m, k, kp, (int)m, xs, tid, [&] { load_batch(wave); });
+    stage_activations<E5, ADT, MT>(a, a_vec, a_scale, a_inv, m, k, kp, (int)m, xs, tid, [&] { load_batch(wave); });
     __syncthreads();
 
     const int fmt = E5 ? 1 : 0;
@@ -174,6 +174,97 @@ __global__ __launch_bounds__(kGemvThreads) void fp8_gemv_mfma_kernel(const void*
                 x1 = *reinterpret_cast<const uint4*>(xrow + s * 128 + 16);
             }
             const v8i av = v8i{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+            const v8i bv = v8i{(int)wb[u][0].x, (int)wb[u][0].y, (int)wb[u][0].z, (int)wb[u][0].w,
+                               (int)wb[u][1].x, (int)wb[u][1].y, (int)wb[u][1].z, (int)wb[u][1].w};
+            acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc, fmt, fmt, 0, 127, 0, 127);
+        }
+    }
+    // C fragment of lane l: column l%16, rows 4*(l/16) .. +3.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][fq * 4 + r][fr] = acc[r];
+    __syncthreads();
+    const int row = tid >> 4, cc = tid & 15;
+    const int64_t col = col0 + cc;
+    if (row < m && col < n) ep.store(red[0][row][cc] + red[1][row][cc] + red[2][row][cc] + red[3][row][cc], row, col);
+}
+
+// Same MFMA GEMV without the LDS staging, for 16-byte aligned activation rows whose length is a multiple of
+// 16 bytes' worth of elements (k % (16 / element size) == 0): each lane
+// loads and encodes exactly the 32 activations of its own A-operand slice (row l%16, K slice l/16 of the
+// step) in registers.  The staging kernel has every thread of a block encode the whole activation
+// matrix into LDS in serial batches and wait at a barrier; here the activation loads of a batch of
+// steps are issued together, ahead of that batch's weight loads, and no barrier precedes the MFMAs.
+template <bool E5, int ADT, int U>
+__global__ __launch_bounds__(kGemvThreads) void fp8_gemv_mfma_reg_kernel(const void* __restrict__ a, float a_scale,
+                                                                          float a_inv, int64_t m, int64_t k,
+                                                                          const uint8_t* __restrict__ w, int64_t kp,
+                                                                          int64_t n, Fp8Epilogue ep) {
+    __shared__ float red[4][16][17];
+    constexpr int esz = ADT == 0 ? 1 : (ADT == 1 ? 2 : 4);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int64_t col0 = (int64_t)blockIdx.x * 16;
+    const int steps = (int)(kp / 128);
+    const int fr = lane & 15;
+    const int fq = lane >> 4;
+    const uint8_t* wcol = w + (col0 + fr) * kp + fq * 32;  // rows past n: zero padding of the prepared weight
+    const bool arow = fr < m;
+    const uint8_t* arow_p = static_cast<const uint8_t*>(a) + (arow ? (int64_t)fr * k * esz : 0);
+    const int fmt = E5 ? 1 : 0;
+    v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    // 16-byte activation loads cover 16 / esz elements: two groups of 4 (bf16), one (fp32), four (fp8)
+    constexpr int kPer16 = 16 / esz / 4;      // groups per 16-byte load
+    constexpr int kLoads = 8 / kPer16;        // 16-byte loads per lane per step
+    for (int s0 = wave; s0 < steps; s0 += 4 * U) {
+        // activation loads of this batch first (L2 hits: their wait then leaves the weight loads in flight);
+        // lanes of rows past m issue none
+        uint4 raw[U][kLoads];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int s = s0 + 4 * u < steps ? s0 + 4 * u : steps - 1;
+#pragma unroll
+            for (int j = 0; j < kLoads; ++j) {
+                const int64_t kk = (int64_t)s * 128 + fq * 32 + j * kPer16 * 4;
+                raw[u][j] = make_uint4(0, 0, 0, 0);
+                if (arow && kk < k) raw[u][j] = *reinterpret_cast<const uint4*>(arow_p + kk * esz);
+            }
+        }
+        uint4 wb[U][2];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int s = s0 + 4 * u;
+            const uint8_t* p = wcol + (int64_t)(s < steps ? s : steps - 1) * 128;  // clamped: unconditional
+            wb[u][0] = load_stream16(p);
+            wb[u][1] = load_stream16(p + 16);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (s0 + 4 * u >= steps) break;  // wave-uniform
+            uint32_t c[8];
+#pragma unroll
+            for (int g = 0; g < 8; ++g) {
+                const uint4 v = raw[u][g / kPer16];
+                const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+                if constexpr (ADT == 0) {
+                    c[g] = w4[g % 4];
+                } else {
+                    float q[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        uint32_t bits;
+                        if constexpr (ADT == 1) {
+                            const uint32_t d = w4[(g % 2) * 2 + (i >> 1)];
+                            bits = i & 1 ? d & 0xffff0000u : d << 16;
+                        } else {
+                            bits = w4[i];
+                        }
+                        q[i] = scale_down(fhip::bits_f32(bits), a_scale, a_inv);
+                    }
+                    c[g] = encode4<E5>(q);  // zero inputs (rows past m, K past k) encode to code 0
+                }
+            }
+            const v8i av = v8i{(int)c[0], (int)c[1], (int)c[2], (int)c[3], (int)c[4], (int)c[5], (int)c[6], (int)c[7]};
             const v8i bv = v8i{(int)wb[u][0].x, (int)wb[u][0].y, (int)wb[u][0].z, (int)wb[u][0].w,
                                (int)wb[u][1].x, (int)wb[u][1].y, (int)wb[u][1].z, (int)wb[u][1].w};
             acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc, fmt, fmt, 0, 127, 0, 127);
@@ -389,11 +480,29 @@ int launch_gemv_t(fhip_context ctx, const void* a, float a_scale, int64_t m, con
         FHIP_CHECK_LAUNCH(ctx, "fp8_gemv1_kernel");
         return FHIP_OK;
     }
+    constexpr int kVecElems = ADT == 0 ? 16 : (ADT == 1 ? 8 : 4);
+    // m <= 4: the LDS-staged kernel (one staging batch; the register kernel's idle rows cost more there)
+    if (m > 4 && m <= 16 && a_vec && w->k % kVecElems == 0) {
+        const unsigned grid = (unsigned)((w->n + 15) / 16);
+        if (kp / 128 <= 8)
+            fp8_gemv_mfma_reg_kernel<E5, ADT, 2><<<grid, kGemvThreads, 0, ctx->stream>>>(a, a_scale, a_inv, m, w->k, wd,
+                                                                                          kp, w->n, ep);
+        else
+            fp8_gemv_mfma_reg_kernel<E5, ADT, 4><<<grid, kGemvThreads, 0, ctx->stream>>>(a, a_scale, a_inv, m, w->k, wd,
+                                                                                          kp, w->n, ep);
+        ctx->last_backend = "fp8_gemv_mfma";
+        FHIP_CHECK_LAUNCH(ctx, "fp8_gemv_mfma_reg_kernel");
+        return FHIP_OK;
+    }
     if (m <= 16) {
         const unsigned grid = (unsigned)((w->n + 15) / 16);
         const size_t lds = (size_t)m * kp;
-        fp8_gemv_mfma_kernel<E5, ADT><<<grid, kGemvThreads, lds, ctx->stream>>>(a, a_vec, a_scale, a_inv, m, w->k, wd,
-                                                                               kp, w->n, ep);
+        if (m <= 4)
+            fp8_gemv_mfma_kernel<E5, ADT, 4><<<grid, kGemvThreads, lds, ctx->stream>>>(a, a_vec, a_scale, a_inv, m, w->k,
+                                                                                      wd, kp, w->n, ep);
+        else
+            fp8_gemv_mfma_kernel<E5, ADT, 16><<<grid, kGemvThreads, lds, ctx->stream>>>(a, a_vec, a_scale, a_inv, m, w->k,
+                                                                                       wd, kp, w->n, ep);
         ctx->last_backend = "fp8_gemv_mfma";
         FHIP_CHECK_LAUNCH(ctx, "fp8_gemv_mfma_kernel");
         return FHIP_OK;

@@ -106,7 +106,7 @@ def test_fp8_gemv_long_k_non_pow2_scale(ctx, dtype, m):
 
 
 @pytest.mark.parametrize("dtype", FP8)
-@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("m", [1, 4, 7, 16])
 def test_fp8_gemv_fused_bf16_io(ctx, dtype, m):
     """bf16 activations -> Cast(fp8) -> MatMul -> Cast(bf16), fused: equals the three-node chain."""
     k, n = 1024, 3584
@@ -304,4 +304,28 @@ def test_fp8_gemm_special_values_and_saturation(ctx, dtype, shape, mode):
     fp8_linear_check(dtype, np.where(keep, got, 0)[ordinary].astype(np.uint8),
                      np.where(keep, ref, 0)[ordinary].astype(np.uint8), a[rows][ordinary], sa, w_nk, sw, s_out,
                      f"special {shape} {mode}")
+    wt.release()
+
+
+@pytest.mark.parametrize("dtype", FP8)
+@pytest.mark.parametrize("m,k", [(9, 1000), (13, 260), (6, 1003)])
+def test_fp8_gemv_fp32_input_ragged_k(ctx, dtype, m, k):
+    """fp32 activations with a non-power-of-two input scale (the encode divides) and K not a multiple of
+    the 128-deep MFMA step; k = 1003 is not a multiple of 4 either (the LDS-staged kernel).  The fused
+    Cast must give the codes of Cast(fp32 -> fp8) of the same rows."""
+    n = 520
+    r = rng(SEEDS[2] + m * 1000 + k)
+    x = r.standard_normal((m, k)).astype(np.float32)
+    w = (r.standard_normal((n, k)) * 0.02).astype(np.float32)
+    w_codes, sw = fp8_tensor(w, dtype)
+    s_in = float(np.float32(np.max(np.abs(x)) / 300.0))
+    a_codes = po.cast_to_fp8(po.FP32, x, dtype, s_in)
+    from tests.common import fp8_pow2_scale
+    s_out = fp8_pow2_scale(float(np.max(np.abs(po.fp8_sums(dtype, a_codes, s_in, w_codes, sw, True)))), dtype)
+    wt = ctx.prepare_weight(dev(w_codes), dtype, k, n, 1, version=8)
+    out = torch.empty((m, n), dtype=torch.uint8, device="cuda")
+    ctx.fp8_linear(dev(x), po.FP32, s_in, m, wt, sw, out, dtype, s_out)
+    assert ctx.last_backend() == "fp8_gemv_mfma"
+    ref = po.fp8_gemm(dtype, a_codes, s_in, w_codes, sw, True, s_out)
+    fp8_linear_check(dtype, host(out), ref, a_codes, s_in, w_codes, sw, s_out, f"gemv fp32 m={m} k={k}")
     wt.release()
