@@ -19,6 +19,7 @@ on the host, M=1 with its prepared (BF16-packed) weight, for a bounded ~10 s sam
 `configs`: the other BASELINE.json configs (C1, C2 M=4/16, C3, C4, C5), same method.
 """
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -204,6 +205,80 @@ def cpu_headline(args):
                   f"M=1 K=1024 N=3584 e4m3, median {med * 1e3:.3f} ms/call; the two memory-bound Cast nodes "
                   f"(1024 + 3584 elements) are not included; host nproc={os.cpu_count()}",
     }
+
+
+def _time_calls(fn, seconds, min_calls=5):
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < min_calls:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_configs(args):
+    """CPU baselines of the other configs on the host cores, each a bounded sample (~3 s).
+    C3 and C5 run the reference's own x86 kernels (oracle/_ref, its thread policy: min(4, OpenMP) workers);
+    C1 and C4 run the C restatement of the reference's Common kernels (oracle/liboracle.so: the x86 INT8
+    FC is single-threaded in the reference, its conv uses every OpenMP thread)."""
+    import numpy as np
+    from oracle import pyoracle as po
+    res = {}
+    budget = max(1.0, args.cpu_seconds / 3.0)
+    r = np.random.default_rng(0xFEA70010)
+    L = po.lib()
+    all_threads = L.fo_set_threads(0)
+    # C1: QuantizeLinear -> INT8 Gemm (transB) -> DequantizeLinear is dominated by the Gemm; 1 thread
+    m, k, n = 128, 1024, 1024
+    a = r.integers(-127, 128, (m, k)).astype(np.int8)
+    w = r.integers(-127, 128, (n, k)).astype(np.int8)
+    ws = r.uniform(1e-3, 1e-2, n).astype(np.float32)
+    bias = r.integers(-20000, 20000, n).astype(np.int32)
+    L.fo_set_threads(1)
+    med, calls = _time_calls(lambda: po.i8_linear(po.I8_GEMM, a, 0.03, 0, w, True, ws, None, bias, po.BIAS_VECTOR, 1.0,
+                                                  1.0, 0.05, 0), budget)
+    res["C1"] = {"value": 2.0 * m * k * n / med / 1e12, "unit": "TOPS", "cores": 1, "kind": "port",
+                 "sample": f"{calls} calls of the INT8 Gemm 128x1024x1024 restated from the Common kernel, "
+                           f"median {med * 1e3:.2f} ms"}
+    # C4: INT8 conv 3x3 s2 p1, all threads
+    L.fo_set_threads(all_threads)
+    x = r.integers(-128, 128, (1, 64, 160, 160)).astype(np.int8)
+    wc = r.integers(-127, 128, (128, 64, 3, 3)).astype(np.int8)
+    wcs = r.uniform(1e-3, 1e-2, 128).astype(np.float32)
+    cb = r.integers(-5000, 5000, 128).astype(np.int32)
+    med, calls = _time_calls(lambda: po.i8_conv2d(x, 0.05, 0, wc, wcs, cb, 2, 1, 0.5, 0), budget)
+    res["C4"] = {"value": 943718400 / med / 1e12, "unit": "TOPS", "cores": all_threads, "kind": "port",
+                 "sample": f"{calls} calls of the INT8 Conv2D [1,64,160,160] x [128,64,3,3] s2 p1 restated from the "
+                           f"Common kernel, median {med * 1e3:.1f} ms"}
+    if po.ref_available():
+        R = po.ref()
+        threads = min(4, R.ref_max_threads())
+        # C3: x86 FP8 linear (direct kernel) on a 32-row sample of the up-projection, e5m2
+        rows, k3, n3 = 32, 1024, 3584
+        a3 = po.fp8_encode(po.FP8E5M2, r.standard_normal((rows, k3)).astype(np.float32))
+        w3 = po.fp8_encode(po.FP8E5M2, (r.standard_normal((n3, k3)) * 0.02 * 2 ** 10).astype(np.float32))
+        y3 = np.empty((rows, n3), np.uint8)
+        med, calls = _time_calls(lambda: R.ref_fp8_linear(po.FP8E5M2, po._ptr(a3), 1.0, po._ptr(w3), 2.0 ** -10, 1,
+                                                          None, 1.0, 0, 1.0, 1.0, rows, k3, n3, po._ptr(y3), 1.0),
+                                 budget)
+        res["C3"] = {"value": 2.0 * rows * k3 * n3 / med / 1e12, "unit": "TFLOP/s", "cores": threads,
+                     "kind": "reference",
+                     "sample": f"{calls} calls of Feather x86 ComputeLinearRowMajorX86Fp8TransposedRhs on {rows} of "
+                               f"the 4096 up-projection rows, median {med * 1e3:.2f} ms"}
+        # C5: x86 BF16 LM-head argmax, M=1 (packed transposed RHS, prepared once)
+        v5, k5 = 151936, 1024
+        w5 = po.bf16_encode((r.standard_normal((v5, k5), dtype=np.float32) * np.float32(0.02)))
+        a5 = po.bf16_encode(r.standard_normal(k5).astype(np.float32))
+        h = R.ref_bf16_argmax_create(po._ptr(w5), k5, v5)
+        tok = ctypes.c_int64()
+        med, calls = _time_calls(lambda: R.ref_bf16_argmax_compute(h, po._ptr(a5), ctypes.byref(tok)), budget)
+        R.ref_bf16_argmax_destroy(h)
+        res["C5"] = {"value": (v5 * k5 * 2 + k5 * 2 + 8) / med / 1e9, "unit": "GB/s", "cores": threads,
+                     "kind": "reference",
+                     "sample": f"{calls} calls of Feather x86 ComputeLinearRowMajorX86Bf16PackedTransposedRhsArgmax, "
+                               f"M=1 K=1024 V=151936, median {med * 1e3:.1f} ms"}
+    return res
 
 
 def vendor_fp8_gemm_us(b, m, k, n):
@@ -429,6 +504,11 @@ def main():
             line["configs_error"] = repr(e)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_headline(args)
+        if not args.only_headline:
+            try:
+                line["cpu_configs"] = cpu_configs(args)
+            except Exception as e:  # report, never hide
+                line["cpu_configs_error"] = repr(e)
     print(json.dumps(line))
 
 
