@@ -172,28 +172,30 @@ def _encode_probe_values(dtype, count, seed):
 
 @pytest.mark.parametrize("dtype", FP8)
 @pytest.mark.parametrize("src", [po.FP32, po.BF16])
-def test_fp8_gemv_m1_activation_encode_exact(ctx, dtype, src):
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_fp8_gemv_m1_activation_encode_exact(ctx, dtype, src, m):
     """With an identity weight (code of 1.0 on the diagonal, w_scale 1) and out_scale = a_scale, every
-    output code equals the activation's own Cast code, so the fused encode inside the M=1 kernel is
-    checked bit-exactly against the reference Cast.  K = N = 1088 (padded 1152) makes the kernel stage
-    the row in two passes and walk the weight row in two chunks per lane."""
+    output code equals the activation's own Cast code, so the fused encode inside the decode kernels is
+    checked bit-exactly against the reference Cast: the M=1 kernel (m = 1), the LDS-staged MFMA kernel
+    (m = 3) and the register-encoding MFMA kernel (m = 8).  K = N = 1088 (padded 1152) makes the M=1
+    kernel stage the row in two passes and walk the weight row in two chunks per lane."""
     k = n = 1088
     s_in = 0.25
-    v = _encode_probe_values(dtype, k, 31)
-    x = (v * np.float32(s_in)).astype(np.float32).reshape(1, k)
+    v = np.stack([_encode_probe_values(dtype, k, 31 + i) for i in range(m)])
+    x = (v * np.float32(s_in)).astype(np.float32).reshape(m, k)
     xin = x if src == po.FP32 else po.bf16_encode(x)
     one = int(po.fp8_encode(dtype, np.array([1.0], np.float32))[0])
     w = np.zeros((k, n), np.uint8)
     w[np.arange(k), np.arange(n)] = one
     wt = ctx.prepare_weight(dev(w), dtype, k, n, 0, version=6)
-    out = torch.empty((1, n), dtype=torch.uint8, device="cuda")
-    ctx.fp8_linear(dev(xin), src, s_in, 1, wt, 1.0, out, dtype, s_in)
-    assert ctx.last_backend() == "fp8_gemv_m1"
+    out = torch.empty((m, n), dtype=torch.uint8, device="cuda")
+    ctx.fp8_linear(dev(xin), src, s_in, m, wt, 1.0, out, dtype, s_in)
+    assert ctx.last_backend() == ("fp8_gemv_m1" if m == 1 else "fp8_gemv_mfma")
     a_codes = po.cast_to_fp8(src, xin, dtype, s_in)
     ref = po.fp8_matmul(dtype, a_codes, s_in, w, 1.0, s_in)
     got = host(out)
-    bad = np.nonzero(got != ref)[1]
-    assert bad.size == 0, f"{bad.size} mismatches: x={x[0, bad[:4]]} got={got[0, bad[:4]]} ref={ref[0, bad[:4]]}"
+    bad = np.nonzero(got != ref)
+    assert bad[0].size == 0, f"{bad[0].size} mismatches: x={x[bad][:4]} got={got[bad][:4]} ref={ref[bad][:4]}"
     wt.release()
 
 
