@@ -143,3 +143,28 @@ def test_fp8_argmax_head(ctx, dtype, m, k):
             # whose sums straddle an FP8 code boundary by accumulation-order rounding.
             vals = vals_all[j]
             assert abs(vals[got] - vals[ref]) <= abs(vals[ref]) * 0.13, (j, got, ref)
+
+
+def test_argmax_two_contexts_concurrent():
+    """Two sessions (one context and stream each) launch argmax calls back to back without waiting for
+    each other: each context's completion ticket and partial keys are its own, so every call's tokens
+    are right however the two streams interleave on the device."""
+    from infer_amd.runtime import Context
+    k, v = 1024, 20000
+    ctxs = [Context(0), Context(0)]
+    cases = []
+    for rnd in range(4):
+        for ci, c in enumerate(ctxs):
+            m = 1 if (rnd + ci) % 2 == 0 else 8
+            a, w = head_inputs(300 + 10 * rnd + ci, m, k, v)
+            tokens = torch.empty(m, dtype=torch.int64, device="cuda")
+            with torch.cuda.stream(c.stream):
+                da, dw = dev(a), dev(w)
+                c.bf16_gemv_argmax(da, dw, tokens)
+            cases.append((a, w, tokens, da, dw))
+    for c in ctxs:
+        c.synchronize()
+    flips = sum(check_tokens(a, w, t.cpu().numpy()) for a, w, t, _, _ in cases)
+    assert flips <= 1
+    for c in ctxs:
+        c.close()
