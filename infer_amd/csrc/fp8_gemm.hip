@@ -450,7 +450,7 @@ int launch_tile(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, cons
     const int tiles = tiles_m * tiles_n;
     const int grid = tiles;  // the kernel remaps tiles XCD-wise
     if (m * k64 >= (int64_t(1) << 31) || np * kp >= (int64_t(1) << 31))
-        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "fp8 gemm: operands of 2 GiB or more");
+        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "fp8 gemm: a prepared weight of 2 GiB or more");
     XcdMap xm{1, 0, 1};
     {
         const int splits[4][2] = {{8, 1}, {4, 2}, {2, 4}, {1, 8}};
@@ -522,5 +522,21 @@ int launch(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, const fhi
 
 int fhip::launch_fp8_gemm(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, const fhip_weight_s* w,
                           const Fp8Epilogue& ep) {
-    return ep.e5 ? launch<true>(ctx, a, m, k64, w, ep) : launch<false>(ctx, a, m, k64, w, ep);
+    // The kernel addresses the activations with 32-bit offsets (buffer resources), so activations of
+    // 2^31 bytes or more run as several launches over row blocks (multiples of 256 rows).
+    const int64_t limit = (int64_t(1) << 31) - 1;
+    const int64_t max_rows = limit / k64 / 256 * 256;
+    if (m * k64 <= limit || max_rows == 0)
+        return ep.e5 ? launch<true>(ctx, a, m, k64, w, ep) : launch<false>(ctx, a, m, k64, w, ep);
+    const int64_t out_bytes = ep.out_dtype == FHIP_FP32 ? 4 : (ep.out_dtype == FHIP_BF16 ? 2 : 1);
+    for (int64_t r0 = 0; r0 < m; r0 += max_rows) {
+        Fp8Epilogue e = ep;
+        e.out = static_cast<uint8_t*>(ep.out) + r0 * ep.n * out_bytes;
+        if (ep.bias_kind == FHIP_BIAS_MATRIX) e.bias = ep.bias + r0 * ep.n;
+        const int64_t rows = m - r0 < max_rows ? m - r0 : max_rows;
+        const int rc = ep.e5 ? launch<true>(ctx, a + r0 * k64, rows, k64, w, e)
+                             : launch<false>(ctx, a + r0 * k64, rows, k64, w, e);
+        if (rc != FHIP_OK) return rc;
+    }
+    return FHIP_OK;
 }
