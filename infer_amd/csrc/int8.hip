@@ -52,10 +52,24 @@ struct I8Epilogue {
     int32_t dq_zp = 0;
     void* out_any = nullptr;
 
+    // Per-output-channel parameters, loadable ahead of the main loop.
+    struct Col {
+        int32_t wsum;
+        int32_t bias;  // vector bias (0 without one; a matrix bias is read per element)
+        float w_scale;
+    };
+    __device__ __forceinline__ Col col_params(int64_t col) const {
+        return Col{wsum[col], bias_kind == FHIP_BIAS_VECTOR ? bias[col] : 0, w_scales[col]};
+    }
+
     __device__ __forceinline__ void store(int32_t raw, int64_t row, int64_t col) const {
-        const int32_t dot = raw - zp_a * wsum[col];
-        const int32_t b = bias_kind == FHIP_BIAS_NONE ? 0 : bias[bias_kind == FHIP_BIAS_VECTOR ? col : row * ldo + col];
-        const double scale = (double)s_a * (double)w_scales[col];
+        store(raw, row, col, col_params(col));
+    }
+
+    __device__ __forceinline__ void store(int32_t raw, int64_t row, int64_t col, const Col& c) const {
+        const int32_t dot = raw - zp_a * c.wsum;
+        const int32_t b = bias_kind == FHIP_BIAS_MATRIX ? bias[row * ldo + col] : c.bias;
+        const double scale = (double)s_a * (double)c.w_scale;
         double real;
         if (kind == FHIP_I8_GEMM) {
             const double acc = alpha * (double)dot + beta * (double)b;
@@ -106,6 +120,11 @@ __global__ __launch_bounds__(256) void i8_gemm_kernel(const int8_t* __restrict__
     const int8_t* bcol[FN];
 #pragma unroll
     for (int j = 0; j < FN; ++j) bcol[j] = b + (col_base + j * 16 + fr) * kp + fk;  // rows padded to 256
+    // Every output element this thread finishes lies in column col_base + tid % TN (256 % TN == 0), so its
+    // channel parameters are loaded here, overlapping the main loop, instead of once per element.
+    static_assert(256 % TN == 0, "epilogue column per thread");
+    const int64_t my_col = col_base + (threadIdx.x % TN);
+    const I8Epilogue::Col my_params = ep.col_params(my_col < n ? my_col : n - 1);
     v4i acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -153,7 +172,7 @@ __global__ __launch_bounds__(256) void i8_gemm_kernel(const int8_t* __restrict__
         const int64_t row = row_base + rr, col = col_base + cc;
         if (row >= m || col >= n) continue;
         const int32_t raw = red[0][rr][cc] + red[1][rr][cc] + red[2][rr][cc] + red[3][rr][cc];
-        ep.store(raw, row, col);
+        ep.store(raw, row, col, my_params);
     }
 }
 
