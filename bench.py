@@ -169,6 +169,43 @@ def headline(b, args):
     return res
 
 
+def dispatch_floor(b, nbytes=3670016, copies=80, per_graph=400, reps=5):
+    """Reference points for a single dispatch of the headline's size, not this library's code: torch's
+    device copy of the same 3.67 MB weight (it also writes 3.67 MB) from rotated buffers, and an empty
+    kernel (torch.cuda._sleep(0)), each one launch per graph node of a replayed torch CUDA graph."""
+    t = b.torch
+    out = {}
+    try:
+        srcs = [t.empty(nbytes, dtype=t.uint8, device="cuda") for _ in range(copies)]
+        dst = t.empty(nbytes, dtype=t.uint8, device="cuda")
+        for name, fn in (("copy_3670016B_us", lambda i: dst.copy_(srcs[i % copies])),
+                         ("empty_kernel_us", lambda i: t.cuda._sleep(0))):
+            s = t.cuda.Stream()
+            s.wait_stream(t.cuda.current_stream())
+            with t.cuda.stream(s):
+                for i in range(3):
+                    fn(i)
+            t.cuda.current_stream().wait_stream(s)
+            g = t.cuda.CUDAGraph()
+            with t.cuda.graph(g):
+                for i in range(per_graph):
+                    fn(i)
+            for _ in range(3):
+                g.replay()
+            t.cuda.synchronize()
+            e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                g.replay()
+            e1.record()
+            t.cuda.synchronize()
+            out[name] = e0.elapsed_time(e1) * 1e3 / (reps * per_graph)
+            del g
+    except Exception as e:  # reference point only: report, do not fail the bench
+        out["error"] = repr(e)[:200]
+    return out
+
+
 def cpu_headline(args):
     """Reference x86 FP8 linear (prepared BF16-packed RHS), M=1, K=1024, N=3584, on host cores."""
     import ctypes
@@ -497,6 +534,7 @@ def main():
             "kernel_ms_event_pairs": h["kernel_ms"], "kernel_ms_event_pairs_median": h["kernel_ms_median"],
         },
         "cpu_baseline": None,
+        "dispatch_reference_points": dispatch_floor(b),
     }
     if not args.only_headline:
         try:
