@@ -35,7 +35,7 @@ FP8_PEAK_TFLOPS = 5000.0
 INT8_PEAK_TOPS = 5000.0
 METRIC = "FP8/INT8 GEMM TOPS (% MFMA peak) + decode GEMV HBM GB/s (% peak), 1 GPU"
 # library backend name of the headline call -> the kernel it launches (as rocprofv3 names it)
-HEADLINE_KERNELS = {"fp8_gemv_m1": "fp8_gemv1_kernel<false, 1, 2, 2>"}
+HEADLINE_KERNELS = {"fp8_gemv_m1": "fp8_gemv1_kernel<false, 1, 2, 2, true, true>"}
 
 
 def parse():

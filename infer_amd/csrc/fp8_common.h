@@ -131,6 +131,20 @@ __device__ __forceinline__ uint32_t encode4(const float (&q)[4]) {
     return packed;
 }
 
+// Hardware FP8 codes of four values, and a running flag whose bit 7 of some byte ends up set when a code
+// is a special one: e4m3 0x7f (NaN, which the non-saturating converter also gives for |x| >= 464 and
+// Inf) or e5m2 exponent 11111 (Inf for |x| >= 61440, NaN).  Values the reference saturates but that
+// round below those thresholds (448 < |x| < 464, 57344 < |x| < 61440) already get the max-finite code.
+// Masked bytes are at most 0x7f / 0x7c, so adding 1 / 4 carries into bit 7 only from an all-ones field.
+template <bool E5>
+__device__ __forceinline__ uint32_t encode4_flag(const float (&q)[4], uint32_t& flag) {
+    int pk = E5 ? __builtin_amdgcn_cvt_pk_bf8_f32(q[0], q[1], 0, false) : __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+    pk = E5 ? __builtin_amdgcn_cvt_pk_bf8_f32(q[2], q[3], pk, true) : __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], pk, true);
+    constexpr uint32_t kMask = E5 ? 0x7c7c7c7cu : 0x7f7f7f7fu, kOne = E5 ? 0x04040404u : 0x01010101u;
+    flag |= ((uint32_t)pk & kMask) + kOne;
+    return (uint32_t)pk;
+}
+
 template <bool E5>
 __device__ __forceinline__ uint32_t encode1(float q) {
     const int pk = E5 ? __builtin_amdgcn_cvt_pk_bf8_f32(q, 0.0f, 0, false) : __builtin_amdgcn_cvt_pk_fp8_f32(q, 0.0f, 0, false);

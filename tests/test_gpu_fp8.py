@@ -331,3 +331,29 @@ def test_fp8_gemv_fp32_input_ragged_k(ctx, dtype, m, k):
     ref = po.fp8_gemm(dtype, a_codes, s_in, w_codes, sw, True, s_out)
     fp8_linear_check(dtype, host(out), ref, a_codes, s_in, w_codes, sw, s_out, f"gemv fp32 m={m} k={k}")
     wt.release()
+
+
+@pytest.mark.parametrize("dtype", FP8)
+@pytest.mark.parametrize("src", [po.FP32, po.BF16])
+@pytest.mark.parametrize("k", [1000, 1004, 2000, 2048])
+def test_fp8_gemv_m1_k_tails(ctx, dtype, src, k):
+    """The M=1 decode kernel with power-of-two scales at K that is a multiple of 16 (2048: 16-byte chunk
+    loads, two chunks per lane) and that is not (1000, 1004, 2000: per-group loads, a partial last chunk):
+    the fused Cast must give the codes of Cast(src -> fp8), and the outputs the FP8 tolerance."""
+    n = 1040
+    r = rng(SEEDS[2] + 7 * k + src)
+    x = r.standard_normal((1, k)).astype(np.float32)
+    xin = x if src == po.FP32 else po.bf16_encode(x)
+    from tests.common import fp8_pow2_scale
+    s_in = fp8_pow2_scale(float(np.max(np.abs(po.bf16_decode(po.bf16_encode(x))))), dtype)
+    a_codes = po.cast_to_fp8(src, xin, dtype, s_in)
+    w = (r.standard_normal((n, k)) * 0.02).astype(np.float32)
+    w_codes, sw = fp8_tensor(w, dtype)
+    s_out = fp8_pow2_scale(float(np.max(np.abs(po.fp8_sums(dtype, a_codes, s_in, w_codes, sw, True)))), dtype)
+    wt = ctx.prepare_weight(dev(w_codes), dtype, k, n, 1, version=10)
+    out = torch.empty((1, n), dtype=torch.uint8, device="cuda")
+    ctx.fp8_linear(dev(xin), src, s_in, 1, wt, sw, out, dtype, s_out)
+    assert ctx.last_backend() == "fp8_gemv_m1"
+    ref = po.fp8_gemm(dtype, a_codes, s_in, w_codes, sw, True, s_out)
+    fp8_linear_check(dtype, host(out), ref, a_codes, s_in, w_codes, sw, s_out, f"gemv m1 k={k}")
+    wt.release()
