@@ -279,6 +279,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
             fb[j][1] = lds_read16<j * 32 * BK>(b1);
         });
     };
+    // The block scale lives in one VGPR for the whole kernel.  Left to the compiler, the kernel-argument
+    // SGPR is copied into a VGPR inside the loop, and that copy gets an lgkmcnt(0) wait in front of it,
+    // which stalls the MFMAs behind the fragment reads issued just before them.
+    int scale_v;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(scale_v) : "s"(mfma_scale));
     auto mfmas = [&](const u32x4_t (&fa)[FM][2], const u32x4_t (&fb)[FN][2]) {
 #pragma unroll
         for (int i = 0; i < FM; ++i)
@@ -289,8 +294,15 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
                 const v8i bv = v8i{(int)fb[j][0].x, (int)fb[j][0].y, (int)fb[j][0].z, (int)fb[j][0].w,
                                    (int)fb[j][1].x, (int)fb[j][1].y, (int)fb[j][1].z, (int)fb[j][1].w};
                 // weight fragment as the row operand: each 32x32 block is computed transposed
-                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[i][j], fmt, fmt, 0, mfma_scale, 0, 127);
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[i][j], fmt, fmt, 0, scale_v, 0, 127);
             }
+        // Pin the MFMAs here: they are pure operations, which IR-level code motion may sink below the
+        // following lgkmcnt fence (sched_barrier binds only the machine scheduler).  Volatile asm keeps
+        // its order with the fence.
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) asm volatile("" : "+v"(acc[i][j]));
     };
     // Wait until at most min(STAGES - 2, nk - 1 - kt) stages issued after stage kt are still in flight.
     auto wait_stage = [&](int kt) {
