@@ -17,6 +17,8 @@ rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated on a copy kernel (profiles/fp8_gem
 `cpu_baseline`: the reference's own x86 FP8 linear (oracle/_ref, built from the Feather sources)
 on the host, M=1 with its prepared (BF16-packed) weight, for a bounded ~10 s sample.
 `configs`: the other BASELINE.json configs (C1, C2 M=4/16, C3, C4, C5), same method.
+`measured_ceilings`: what the chip sustains beside the published peaks -- the FP8 MFMA rate with the C3
+operand codes (and with zero codes) in the registers, and the L2 -> LDS staging rate (ceilings()).
 """
 import argparse
 import ctypes
@@ -487,6 +489,33 @@ def extra_configs(b, args):
     return res
 
 
+def ceilings(b):
+    """Measured ceilings beside the published peaks (infer_amd/ceilings.hip, not part of the operator
+    library): the sustained FP8 MFMA rate with the C3 activation codes, and with all-zero codes, in the
+    operand registers (MFMA power, and so the sustained clock, depends on the operand bits), and the
+    L2 -> LDS rate of the GEMM's operand staging path over an L2-resident 2 MB buffer."""
+    t, L = b.torch, b.L
+    lib = ctypes.CDLL(os.path.join(ROOT, "infer_amd", "libfhip_ceilings.so"))
+    lib.fhipc_mfma_fp8_rate.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                        ctypes.POINTER(ctypes.c_float)]
+    lib.fhipc_l2_stream.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.POINTER(ctypes.c_float)]
+    codes, _ = b.to_fp8(b.randn((4096, 1024), 0xFEA70003), L.FP8E5M2)  # the C3 activations
+    zeros = t.zeros(1 << 16, dtype=t.uint8, device="cuda")
+    buf = t.ones(2 << 20, dtype=t.uint8, device="cuda")
+    t.cuda.synchronize()
+    out = {}
+    for name, src in (("mfma_fp8_tflops_c3_operands", codes), ("mfma_fp8_tflops_zero_operands", zeros)):
+        v = ctypes.c_float(0.0)
+        rc = lib.fhipc_mfma_fp8_rate(src.data_ptr(), src.numel(), 1, 4000, ctypes.byref(v))
+        out[name] = round(v.value, 1) if rc == 0 else f"error {rc}"
+    v = ctypes.c_float(0.0)
+    rc = lib.fhipc_l2_stream(buf.data_ptr(), buf.numel(), 400, ctypes.byref(v))
+    out["l2_to_lds_tbs"] = round(v.value, 2) if rc == 0 else f"error {rc}"
+    out["note"] = ("mfma: one 512-thread block per CU, 4 independent v_mfma_scale_f32_32x32x64_f8f6f4 chains; "
+                   "l2: 16-byte buffer_load...lds, one 512-thread block per CU, 2 MB L2-resident buffer")
+    return out
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
     (profiles/fp8_gemv_decode_m1.traffic.json), or None when that summary is of another kernel."""
@@ -541,6 +570,11 @@ def main():
             line["configs"] = extra_configs(b, args)
         except Exception as e:  # report, never hide, a failing extra config
             line["configs_error"] = repr(e)
+    if not args.only_headline:
+        try:
+            line["measured_ceilings"] = ceilings(b)
+        except Exception as e:  # report, never hide
+            line["measured_ceilings_error"] = repr(e)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_headline(args)
         if not args.only_headline:
