@@ -194,7 +194,11 @@ __global__ __launch_bounds__(kGemvThreads) void fp8_gemv_mfma_kernel(const void*
 // step) in registers.  The staging kernel has every thread of a block encode the whole activation
 // matrix into LDS in serial batches and wait at a barrier; here the activation loads of a batch of
 // steps are issued together, ahead of that batch's weight loads, and no barrier precedes the MFMAs.
-template <bool E5, int ADT, int U>
+// POW2: a_inv != 0 (power-of-two activation scale), so x / s is x * (1/s) exactly and no division is compiled.
+// Encoding: the hardware converter's codes for the whole batch with a running special-code flag
+// (encode4_flag, no branch); a lane whose batch met a value beyond the largest finite code, Inf or NaN
+// re-encodes the batch with the reference's saturated / special codes (encode4) in one cold branch.
+template <bool E5, int ADT, int U, bool POW2>
 __global__ __launch_bounds__(kGemvThreads) void fp8_gemv_mfma_reg_kernel(const void* __restrict__ a, float a_scale,
                                                                           float a_inv, int64_t m, int64_t k,
                                                                           const uint8_t* __restrict__ w, int64_t kp,
@@ -238,33 +242,54 @@ __global__ __launch_bounds__(kGemvThreads) void fp8_gemv_mfma_reg_kernel(const v
             wb[u][0] = load_stream16(p);
             wb[u][1] = load_stream16(p + 16);
         }
+        // activation codes of the whole batch: hot pass with the hardware converter, one cold fix-up branch
+        auto act = [&](int u, int g, int i) -> float {
+            const uint4 v = raw[u][g / kPer16];
+            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+            uint32_t bits;
+            if constexpr (ADT == 1) {
+                const uint32_t d = w4[(g % 2) * 2 + (i >> 1)];
+                bits = i & 1 ? d & 0xffff0000u : d << 16;
+            } else {
+                bits = w4[i];
+            }
+            const float x = fhip::bits_f32(bits);
+            return POW2 ? x * a_inv : x / a_scale;
+        };
+        uint32_t c[U][8];
+        if constexpr (ADT == 0) {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int g = 0; g < 8; ++g) {
+                    const uint4 v = raw[u][g / kPer16];
+                    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+                    c[u][g] = w4[g % 4];
+                }
+        } else {
+            uint32_t flag = 0;
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int g = 0; g < 8; ++g) {
+                    const float q[4] = {act(u, g, 0), act(u, g, 1), act(u, g, 2), act(u, g, 3)};
+                    c[u][g] = encode4_flag<E5>(q, flag);  // zero inputs (rows past m, K past k) encode to 0
+                }
+            if (__builtin_expect((flag & 0x80808080u) != 0, 0)) {
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+#pragma unroll
+                    for (int g = 0; g < 8; ++g) {
+                        const float q[4] = {act(u, g, 0), act(u, g, 1), act(u, g, 2), act(u, g, 3)};
+                        c[u][g] = encode4<E5>(q);
+                    }
+            }
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (s0 + 4 * u >= steps) break;  // wave-uniform
-            uint32_t c[8];
-#pragma unroll
-            for (int g = 0; g < 8; ++g) {
-                const uint4 v = raw[u][g / kPer16];
-                const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-                if constexpr (ADT == 0) {
-                    c[g] = w4[g % 4];
-                } else {
-                    float q[4];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        uint32_t bits;
-                        if constexpr (ADT == 1) {
-                            const uint32_t d = w4[(g % 2) * 2 + (i >> 1)];
-                            bits = i & 1 ? d & 0xffff0000u : d << 16;
-                        } else {
-                            bits = w4[i];
-                        }
-                        q[i] = scale_down(fhip::bits_f32(bits), a_scale, a_inv);
-                    }
-                    c[g] = encode4<E5>(q);  // zero inputs (rows past m, K past k) encode to code 0
-                }
-            }
-            const v8i av = v8i{(int)c[0], (int)c[1], (int)c[2], (int)c[3], (int)c[4], (int)c[5], (int)c[6], (int)c[7]};
+            const v8i av = v8i{(int)c[u][0], (int)c[u][1], (int)c[u][2], (int)c[u][3], (int)c[u][4], (int)c[u][5],
+                               (int)c[u][6], (int)c[u][7]};
             const v8i bv = v8i{(int)wb[u][0].x, (int)wb[u][0].y, (int)wb[u][0].z, (int)wb[u][0].w,
                                (int)wb[u][1].x, (int)wb[u][1].y, (int)wb[u][1].z, (int)wb[u][1].w};
             acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc, fmt, fmt, 0, 127, 0, 127);
@@ -554,12 +579,18 @@ int launch_gemv_t(fhip_context ctx, const void* a, float a_scale, int64_t m, con
     // m <= 4: the LDS-staged kernel (one staging batch; the register kernel's idle rows cost more there)
     if (m > 4 && m <= 16 && a_vec && w->k % kVecElems == 0) {
         const unsigned grid = (unsigned)((w->n + 15) / 16);
-        if (kp / 128 <= 8)
-            fp8_gemv_mfma_reg_kernel<E5, ADT, 2><<<grid, kGemvThreads, 0, ctx->stream>>>(a, a_scale, a_inv, m, w->k, wd,
-                                                                                          kp, w->n, ep);
-        else
-            fp8_gemv_mfma_reg_kernel<E5, ADT, 4><<<grid, kGemvThreads, 0, ctx->stream>>>(a, a_scale, a_inv, m, w->k, wd,
-                                                                                          kp, w->n, ep);
+#define FHIP_REG_LAUNCH(U, P2)                                                                                    \
+    fp8_gemv_mfma_reg_kernel<E5, ADT, U, P2><<<grid, kGemvThreads, 0, ctx->stream>>>(a, a_scale, a_inv, m, w->k, wd, kp, \
+                                                                                     w->n, ep)
+        const bool p2 = a_inv != 0.0f;
+        if (kp / 128 <= 8) {
+            if (p2) FHIP_REG_LAUNCH(2, true);
+            else FHIP_REG_LAUNCH(2, false);
+        } else {
+            if (p2) FHIP_REG_LAUNCH(4, true);
+            else FHIP_REG_LAUNCH(4, false);
+        }
+#undef FHIP_REG_LAUNCH
         ctx->last_backend = "fp8_gemv_mfma";
         FHIP_CHECK_LAUNCH(ctx, "fp8_gemv_mfma_reg_kernel");
         return FHIP_OK;
