@@ -576,8 +576,8 @@ int launch_gemv_t(fhip_context ctx, const void* a, float a_scale, int64_t m, con
         return FHIP_OK;
     }
     constexpr int kVecElems = ADT == 0 ? 16 : (ADT == 1 ? 8 : 4);
-    // m <= 4: the LDS-staged kernel (one staging batch; the register kernel's idle rows cost more there)
-    if (m > 4 && m <= 16 && a_vec && w->k % kVecElems == 0) {
+    // 2 <= m <= 16 with aligned activation rows: the register kernel; otherwise the LDS-staged kernel
+    if (m > 1 && m <= 16 && a_vec && w->k % kVecElems == 0) {
         const unsigned grid = (unsigned)((w->n + 15) / 16);
 #define FHIP_REG_LAUNCH(U, P2)                                                                                    \
     fp8_gemv_mfma_reg_kernel<E5, ADT, U, P2><<<grid, kGemvThreads, 0, ctx->stream>>>(a, a_scale, a_inv, m, w->k, wd, kp, \

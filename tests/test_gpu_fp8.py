@@ -172,13 +172,14 @@ def _encode_probe_values(dtype, count, seed):
 
 @pytest.mark.parametrize("dtype", FP8)
 @pytest.mark.parametrize("src", [po.FP32, po.BF16])
-@pytest.mark.parametrize("m", [1, 3, 8])
-def test_fp8_gemv_m1_activation_encode_exact(ctx, dtype, src, m):
+@pytest.mark.parametrize("m,staged", [(1, False), (3, False), (8, False), (3, True)])
+def test_fp8_gemv_m1_activation_encode_exact(ctx, dtype, src, m, staged):
     """With an identity weight (code of 1.0 on the diagonal, w_scale 1) and out_scale = a_scale, every
     output code equals the activation's own Cast code, so the fused encode inside the decode kernels is
-    checked bit-exactly against the reference Cast: the M=1 kernel (m = 1), the LDS-staged MFMA kernel
-    (m = 3) and the register-encoding MFMA kernel (m = 8).  K = N = 1088 (padded 1152) makes the M=1
-    kernel stage the row in two passes and walk the weight row in two chunks per lane."""
+    checked bit-exactly against the reference Cast: the M=1 kernel (m = 1) and the register-encoding MFMA
+    kernel (m = 3, 8); with `staged`, activation rows that start off a 16-byte boundary take the
+    LDS-staged MFMA kernel.  K = N = 1088 (padded 1152) makes the M=1 kernel stage the row in two passes
+    and walk the weight row in two chunks per lane."""
     k = n = 1088
     s_in = 0.25
     v = np.stack([_encode_probe_values(dtype, k, 31 + i) for i in range(m)])
@@ -189,7 +190,12 @@ def test_fp8_gemv_m1_activation_encode_exact(ctx, dtype, src, m):
     w[np.arange(k), np.arange(n)] = one
     wt = ctx.prepare_weight(dev(w), dtype, k, n, 0, version=6)
     out = torch.empty((m, n), dtype=torch.uint8, device="cuda")
-    ctx.fp8_linear(dev(xin), src, s_in, m, wt, 1.0, out, dtype, s_in)
+    xd = dev(xin)
+    if staged:  # same rows, one element past a 16-byte boundary
+        buf = torch.zeros(xd.numel() + 8, dtype=xd.dtype, device="cuda")
+        buf[1:1 + xd.numel()] = xd.reshape(-1)
+        xd = buf[1:1 + xd.numel()].view(m, k)
+    ctx.fp8_linear(xd, src, s_in, m, wt, 1.0, out, dtype, s_in)
     assert ctx.last_backend() == ("fp8_gemv_m1" if m == 1 else "fp8_gemv_mfma")
     a_codes = po.cast_to_fp8(src, xin, dtype, s_in)
     ref = po.fp8_matmul(dtype, a_codes, s_in, w, 1.0, s_in)
