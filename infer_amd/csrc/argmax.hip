@@ -338,8 +338,11 @@ __global__ __launch_bounds__(kThreads) void gemv_argmax_mfma_kernel(const uint8_
         for (int s = 0; s < SPW; ++s)
 #pragma unroll
             for (int q = 0; q < NV; ++q) {
+                // masked, not selected: a select lets the compiler branch around each load and wait for
+                // it inside the branch, serializing the activation loads
                 const uint4 x = *reinterpret_cast<const uint4*>(ar + off[s] + 16 * q);
-                xa[s][q] = (arow && live[s]) ? x : make_uint4(0, 0, 0, 0);
+                const uint32_t msk = (arow && live[s]) ? 0xffffffffu : 0u;
+                xa[s][q] = make_uint4(x.x & msk, x.y & msk, x.z & msk, x.w & msk);
             }
     }
     const int64_t ntiles = (v + 15) / 16;
