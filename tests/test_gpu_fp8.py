@@ -135,7 +135,7 @@ def test_fp8_gemv_fused_bf16_io(ctx, dtype, m):
 
 @pytest.mark.parametrize("dtype", FP8)
 @pytest.mark.parametrize("shape", [(256, 1024, 512), (100, 384, 200), (200, 320, 300), (300, 128, 520),
-                                   (4096, 1024, 3584), (4000, 1152, 3584)])
+                                   (4096, 1024, 3584), (4000, 1152, 3584), (4096, 3584, 1024)])
 def test_fp8_mfma_gemm_matches_oracle(ctx, dtype, shape):
     m, k, n = shape
     a, sa, w_nk, w_src, sw, s_out = _linear_case(SEEDS[3] + m, dtype, m, k, n, 1)
