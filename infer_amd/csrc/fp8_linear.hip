@@ -198,12 +198,14 @@ __global__ __launch_bounds__(kGemvThreads) void fp8_gemv_mfma_kernel(const void*
 // Encoding: the hardware converter's codes for the whole batch with a running special-code flag
 // (encode4_flag, no branch); a lane whose batch met a value beyond the largest finite code, Inf or NaN
 // re-encodes the batch with the reference's saturated / special codes (encode4) in one cold branch.
-template <bool E5, int ADT, int U, bool POW2>
-__global__ __launch_bounds__(kGemvThreads) void fp8_gemv_mfma_reg_kernel(const void* __restrict__ a, float a_scale,
+// NW waves split K (wave w takes the steps w, w + NW, ...), U steps per load batch; the NW partial 16x16
+// tiles are summed through LDS.
+template <bool E5, int ADT, int U, bool POW2, int NW>
+__global__ __launch_bounds__(NW * 64) void fp8_gemv_mfma_reg_kernel(const void* __restrict__ a, float a_scale,
                                                                           float a_inv, int64_t m, int64_t k,
                                                                           const uint8_t* __restrict__ w, int64_t kp,
                                                                           int64_t n, Fp8Epilogue ep) {
-    __shared__ float red[4][16][17];
+    __shared__ float red[NW][16][17];
     constexpr int esz = ADT == 0 ? 1 : (ADT == 1 ? 2 : 4);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -220,13 +222,13 @@ __global__ __launch_bounds__(kGemvThreads) void fp8_gemv_mfma_reg_kernel(const v
     // 16-byte activation loads cover 16 / esz elements: two groups of 4 (bf16), one (fp32), four (fp8)
     constexpr int kPer16 = 16 / esz / 4;      // groups per 16-byte load
     constexpr int kLoads = 8 / kPer16;        // 16-byte loads per lane per step
-    for (int s0 = wave; s0 < steps; s0 += 4 * U) {
+    for (int s0 = wave; s0 < steps; s0 += NW * U) {
         // activation loads of this batch first (L2 hits: their wait then leaves the weight loads in flight);
         // lanes of rows past m issue none
         uint4 raw[U][kLoads];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int s = s0 + 4 * u < steps ? s0 + 4 * u : steps - 1;
+            const int s = s0 + NW * u < steps ? s0 + NW * u : steps - 1;
 #pragma unroll
             for (int j = 0; j < kLoads; ++j) {
                 const int64_t kk = (int64_t)s * 128 + fq * 32 + j * kPer16 * 4;
@@ -237,7 +239,7 @@ __global__ __launch_bounds__(kGemvThreads) void fp8_gemv_mfma_reg_kernel(const v
         uint4 wb[U][2];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int s = s0 + 4 * u;
+            const int s = s0 + NW * u;
             const uint8_t* p = wcol + (int64_t)(s < steps ? s : steps - 1) * 128;  // clamped: unconditional
             wb[u][0] = load_stream16(p);
             wb[u][1] = load_stream16(p + 16);
@@ -287,7 +289,7 @@ __global__ __launch_bounds__(kGemvThreads) void fp8_gemv_mfma_reg_kernel(const v
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            if (s0 + 4 * u >= steps) break;  // wave-uniform
+            if (s0 + NW * u >= steps) break;  // wave-uniform
             const v8i av = v8i{(int)c[u][0], (int)c[u][1], (int)c[u][2], (int)c[u][3], (int)c[u][4], (int)c[u][5],
                                (int)c[u][6], (int)c[u][7]};
             const v8i bv = v8i{(int)wb[u][0].x, (int)wb[u][0].y, (int)wb[u][0].z, (int)wb[u][0].w,
@@ -299,9 +301,14 @@ __global__ __launch_bounds__(kGemvThreads) void fp8_gemv_mfma_reg_kernel(const v
 #pragma unroll
     for (int r = 0; r < 4; ++r) red[wave][fq * 4 + r][fr] = acc[r];
     __syncthreads();
-    const int row = tid >> 4, cc = tid & 15;
-    const int64_t col = col0 + cc;
-    if (row < m && col < n) ep.store(red[0][row][cc] + red[1][row][cc] + red[2][row][cc] + red[3][row][cc], row, col);
+    if (tid < 256) {
+        const int row = tid >> 4, cc = tid & 15;
+        const int64_t col = col0 + cc;
+        float sum = red[0][row][cc];
+#pragma unroll
+        for (int q = 1; q < NW; ++q) sum += red[q][row][cc];
+        if (row < m && col < n) ep.store(sum, row, col);
+    }
 }
 
 // ---- M = 1 decode GEMV, the common case ---------------------------------------------------------
@@ -579,16 +586,18 @@ int launch_gemv_t(fhip_context ctx, const void* a, float a_scale, int64_t m, con
     // 2 <= m <= 16 with aligned activation rows: the register kernel; otherwise the LDS-staged kernel
     if (m > 1 && m <= 16 && a_vec && w->k % kVecElems == 0) {
         const unsigned grid = (unsigned)((w->n + 15) / 16);
+        // 8 waves split K (one 128-deep step each per batch at K <= 1024), so each lane encodes 32 activations
+        // per step of its own and two waves per SIMD cover each other's encode latency
 #define FHIP_REG_LAUNCH(U, P2)                                                                                    \
-    fp8_gemv_mfma_reg_kernel<E5, ADT, U, P2><<<grid, kGemvThreads, 0, ctx->stream>>>(a, a_scale, a_inv, m, w->k, wd, kp, \
-                                                                                     w->n, ep)
+    fp8_gemv_mfma_reg_kernel<E5, ADT, U, P2, 8><<<grid, 8 * 64, 0, ctx->stream>>>(a, a_scale, a_inv, m, w->k, wd, kp, \
+                                                                                  w->n, ep)
         const bool p2 = a_inv != 0.0f;
         if (kp / 128 <= 8) {
+            if (p2) FHIP_REG_LAUNCH(1, true);
+            else FHIP_REG_LAUNCH(1, false);
+        } else {
             if (p2) FHIP_REG_LAUNCH(2, true);
             else FHIP_REG_LAUNCH(2, false);
-        } else {
-            if (p2) FHIP_REG_LAUNCH(4, true);
-            else FHIP_REG_LAUNCH(4, false);
         }
 #undef FHIP_REG_LAUNCH
         ctx->last_backend = "fp8_gemv_mfma";
