@@ -91,18 +91,19 @@ struct I8Epilogue {
 };
 
 // ---- INT8 GEMM: A [m][k] int8 row-major, B prepared [Np][Kp] ---------------------------------
-// Block tile (16*FM) x (16*FN).  The four waves split K: wave w takes the 64-deep steps w, w+4, ...,
-// issues the loads of kUnroll steps before their MFMAs (one memory round trip per kUnroll*4 steps),
-// and the four partial tiles are summed through LDS; integer sums are exact in any order.
+// Block tile (16*FM) x (16*FN).  The NW waves split K: wave w takes the 64-deep steps w, w+NW, ...,
+// issues the loads of UNR steps before their MFMAs (one memory round trip per UNR*NW steps), and the
+// NW partial tiles are summed through LDS; integer sums are exact in any order.
 // MFMA depth 64: lane l supplies row/col l%16 and bytes [16*(l/16), 16*(l/16)+16) of the step.
 constexpr int kI8Unroll = 4;
 
-template <int FM, int FN>
-__global__ __launch_bounds__(256) void i8_gemm_kernel(const int8_t* __restrict__ a, int64_t m, int64_t k,
+template <int FM, int FN, int NW = 4, int UNR = kI8Unroll>
+__global__ __launch_bounds__(NW * 64) void i8_gemm_kernel(const int8_t* __restrict__ a, int64_t m, int64_t k,
                                                       const int8_t* __restrict__ b, int64_t kp, int64_t n,
                                                       I8Epilogue ep) {
     constexpr int TM = 16 * FM, TN = 16 * FN;
-    __shared__ int32_t red[4][TM][TN + 1];
+    constexpr int NT = NW * 64;
+    __shared__ int32_t red[NW][TM][TN + 1];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int64_t row_base = (int64_t)blockIdx.y * TM;
@@ -120,9 +121,9 @@ __global__ __launch_bounds__(256) void i8_gemm_kernel(const int8_t* __restrict__
     const int8_t* bcol[FN];
 #pragma unroll
     for (int j = 0; j < FN; ++j) bcol[j] = b + (col_base + j * 16 + fr) * kp + fk;  // rows padded to 256
-    // Every output element this thread finishes lies in column col_base + tid % TN (256 % TN == 0), so its
+    // Every output element this thread finishes lies in column col_base + tid % TN (NT % TN == 0), so its
     // channel parameters are loaded here, overlapping the main loop, instead of once per element.
-    static_assert(256 % TN == 0, "epilogue column per thread");
+    static_assert(NT % TN == 0, "epilogue column per thread");
     const int64_t my_col = col_base + (threadIdx.x % TN);
     const I8Epilogue::Col my_params = ep.col_params(my_col < n ? my_col : n - 1);
     v4i acc[FM][FN];
@@ -131,11 +132,11 @@ __global__ __launch_bounds__(256) void i8_gemm_kernel(const int8_t* __restrict__
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
     const int64_t steps = (k + 63) / 64;
-    for (int64_t s0 = wave; s0 < steps; s0 += 4 * kI8Unroll) {
-        v4i af[kI8Unroll][FM], bf[kI8Unroll][FN];
+    for (int64_t s0 = wave; s0 < steps; s0 += NW * UNR) {
+        v4i af[UNR][FM], bf[UNR][FN];
 #pragma unroll
-        for (int u = 0; u < kI8Unroll; ++u) {
-            const int64_t s = s0 + 4 * u;
+        for (int u = 0; u < UNR; ++u) {
+            const int64_t s = s0 + NW * u;
             const int64_t k0 = s * 64;
             const bool live = s < steps;
 #pragma unroll
@@ -152,7 +153,7 @@ __global__ __launch_bounds__(256) void i8_gemm_kernel(const int8_t* __restrict__
             }
         }
 #pragma unroll
-        for (int u = 0; u < kI8Unroll; ++u)
+        for (int u = 0; u < UNR; ++u)
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -167,11 +168,13 @@ __global__ __launch_bounds__(256) void i8_gemm_kernel(const int8_t* __restrict__
 #pragma unroll
             for (int r = 0; r < 4; ++r) red[wave][i * 16 + (lane >> 4) * 4 + r][j * 16 + fr] = acc[i][j][r];
     __syncthreads();
-    for (int e = threadIdx.x; e < TM * TN; e += 256) {
+    for (int e = threadIdx.x; e < TM * TN; e += NT) {
         const int rr = e / TN, cc = e % TN;
         const int64_t row = row_base + rr, col = col_base + cc;
         if (row >= m || col >= n) continue;
-        const int32_t raw = red[0][rr][cc] + red[1][rr][cc] + red[2][rr][cc] + red[3][rr][cc];
+        int32_t raw = red[0][rr][cc];
+#pragma unroll
+        for (int q = 1; q < NW; ++q) raw += red[q][rr][cc];
         ep.store(raw, row, col, my_params);
     }
 }
@@ -681,7 +684,7 @@ int fhip_i8_linear_ex(fhip_context ctx, int kind, const int8_t* a, float s_a, in
         ctx->last_backend = "i8_mfma_gemm_32x32_ksplit4";
     } else {
         dim3 grid((unsigned)((w->n + 31) / 32), (unsigned)((m + 15) / 16));
-        i8_gemm_kernel<1, 2><<<grid, 256, 0, ctx->stream>>>(a, m, w->k, bw, kp, w->n, ep);
+        i8_gemm_kernel<1, 2, 8, 2><<<grid, 512, 0, ctx->stream>>>(a, m, w->k, bw, kp, w->n, ep);
         ctx->last_backend = "i8_mfma_gemm_16x32_ksplit4";
     }
     FHIP_CHECK_LAUNCH(ctx, "i8_gemm_kernel");
