@@ -12,3 +12,10 @@ def test_bench_refuses_more_than_one_gpu():
     assert r.returncode == 2
     assert "one GPU only" in r.stderr
     assert r.stdout == ""
+
+
+def test_ceilings_library_exports_its_entry_points():
+    """bench.py's measured ceilings come from a separate diagnostic library built beside libfhip.so."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "infer_amd", "libfhip_ceilings.so"))
+    assert hasattr(lib, "fhipc_mfma_fp8_rate") and hasattr(lib, "fhipc_l2_stream")
