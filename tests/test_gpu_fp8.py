@@ -207,11 +207,12 @@ def test_fp8_gemv_m1_activation_encode_exact(ctx, dtype, src, m, staged):
 
 @pytest.mark.parametrize("dtype", FP8)
 @pytest.mark.parametrize("out_dtype", [po.BF16, po.FP32])
-def test_fp8_gemm_decoded_outputs(ctx, dtype, out_dtype):
+@pytest.mark.parametrize("shape", [(300, 3584, 1024), (4096, 1024, 3584)])
+def test_fp8_gemm_decoded_outputs(ctx, dtype, out_dtype, shape):
     """BF16 / FP32 outputs (the FP8 code decoded with out_scale, as the exported Gemm -> Cast pair) on a
-    down-projection-like shape (K = 3584, 128-deep stages): each output must be exactly a decoded FP8 code
-    and those codes meet the FP8 tolerance."""
-    m, k, n = 300, 3584, 1024
+    down-projection-like shape (K = 3584, 128-deep stages) and the up-projection shape (BF16: 256x224
+    tiles): each output must be exactly a decoded FP8 code and those codes meet the FP8 tolerance."""
+    m, k, n = shape
     a, sa, w_nk, w_src, sw, s_out = _linear_case(SEEDS[3] + 17, dtype, m, k, n, 1)
     wt = ctx.prepare_weight(dev(w_src), dtype, k, n, 1, version=8)
     tdt = torch.int16 if out_dtype == po.BF16 else torch.float32
@@ -241,6 +242,28 @@ def test_fp8_gemm_bias_alpha_beta(ctx):
         ref = po.fp8_gemm(dtype, a[:mm], sa, w_nk, sw, True, s_out, bias=bias, s_bias=sb, bias_kind=po.BIAS_VECTOR,
                           alpha=0.5, beta=2.0)
         assert fp8_code_distance(host(out), ref).max() <= 1  # |sums| >> bias: no near-zero cancellation
+    wt.release()
+
+
+def test_fp8_gemm_bias_alpha_beta_full_size(ctx):
+    """Bias, alpha and beta on the up-projection shape (256x224 tiles, power-of-two output scale with a
+    bias: the unfolded epilogue); a seeded subset of rows against the oracle."""
+    dtype = po.FP8E5M2
+    m, k, n = 4096, 1024, 3584
+    a, sa, w_nk, w_src, sw, s_out = _linear_case(13, dtype, m, k, n, 1)
+    bias_f = rng(14).standard_normal(n).astype(np.float32) * 0.1
+    bias, sb = fp8_tensor(bias_f, dtype)
+    wt = ctx.prepare_weight(dev(w_src), dtype, k, n, 1, version=9)
+    out = torch.empty((m, n), dtype=torch.uint8, device="cuda")
+    ctx.fp8_linear(dev(a), dtype, sa, m, wt, sw, out, dtype, s_out, bias=dev(bias), bias_scale=sb,
+                   bias_kind=po.BIAS_VECTOR, alpha=0.5, beta=2.0)
+    assert ctx.last_backend() == "fp8_mfma_gemm_256x224_bk128_w8"
+    rows = np.union1d(rng(15).choice(m, 64, replace=False), np.arange(m - 4, m))
+    ref = po.fp8_gemm(dtype, a[rows], sa, w_nk, sw, True, s_out, bias=bias, s_bias=sb, bias_kind=po.BIAS_VECTOR,
+                      alpha=0.5, beta=2.0)
+    # the bias is added after the sum, in the reference's order, so only the sum's accumulation order differs;
+    # alpha < 1 scales that error down, so the unscaled bound of fp8_linear_check holds
+    fp8_linear_check(dtype, host(out)[rows], ref, a[rows], sa, w_nk, sw, s_out, "gemm bias full size")
     wt.release()
 
 
