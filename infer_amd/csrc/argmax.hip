@@ -428,13 +428,18 @@ int launch(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k, const uint8
     (void)hipDeviceGetAttribute(&dev_cus, hipDeviceAttributeMultiprocessorCount, ctx->device);
     const int64_t rows_per_block = (int64_t)kWaves * kRows;
     int64_t grid = (v + rows_per_block - 1) / rows_per_block;
-#ifndef FHIP_ARGMAX_BLOCKS_PER_CU
-#define FHIP_ARGMAX_BLOCKS_PER_CU 2
-#endif
-    const int64_t cap = (int64_t)dev_cus * FHIP_ARGMAX_BLOCKS_PER_CU;  // grid-stride over the vocabulary
-    if (grid > cap) grid = cap;
+    // grid-stride over the vocabulary; measured on the C5 head: the MFMA kernel (m >= 2) is fastest with 2
+    // blocks per CU (1, 3, 4: 79, 68, 77 us against 62), the m = 1 kernel with 1 (54.2 against 55.1 us)
+    const int64_t cap = (int64_t)dev_cus * 2;
+    const int64_t cap1 = (int64_t)dev_cus;
+    if (grid > cap1) grid = cap1;
+    // per-block partial keys of either kernel (sized for the larger grid, so a later call with other rows
+    // does not need a bigger workspace, e.g. under capture)
+    int64_t ws_blocks = (v + 15) / 16;
+    if (ws_blocks > cap) ws_blocks = cap;
+    if (ws_blocks < grid) ws_blocks = grid;
     void* ws = nullptr;
-    int rc = fhip::acquire_workspace(ctx, (size_t)grid * 16 * sizeof(unsigned long long), &ws);
+    int rc = fhip::acquire_workspace(ctx, (size_t)ws_blocks * 16 * sizeof(unsigned long long), &ws);
     if (rc != FHIP_OK) return rc;
     auto* partials = static_cast<unsigned long long*>(ws);
     const int64_t bytes = k * (KIND == 0 ? 2 : 1);
