@@ -47,6 +47,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=400)
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--only-headline", action="store_true")
+    p.add_argument("--trace-headline", action="store_true",
+                   help="headline only, graph-replayed launches only (no eager event pairs or dispatch reference "
+                        "points): the run rocprofv3 traces for the headline kernel's per-dispatch duration")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--configs", default="", help="comma list of extra configs to run (C1..C5; default all)")
     return p.parse_args()
@@ -87,12 +90,13 @@ class Bench:
         return out
 
     # -- timing ---------------------------------------------------------------------------------
-    def graph_time(self, steps, reps, warm=3):
+    def graph_time(self, steps, reps, warm=3, eager_warm=True):
         """steps: callables, each enqueues one step on ctx.stream.  Returns ms per step."""
         t, ctx = self.torch, self.ctx
         with t.cuda.stream(self.s):
-            for f in steps:  # eager warm-up grows workspaces before capture
-                f()
+            if eager_warm:
+                for f in steps:  # eager warm-up grows workspaces before capture
+                    f()
             ctx.synchronize()
             ctx.capture_begin()
             for f in steps:
@@ -151,15 +155,20 @@ def headline(b, args):
     ctx.synchronize()
     backend = None
     with t.cuda.stream(b.s):
-        step(0)
+        step(0)  # the one eager call: names the kernel path (the GEMV needs no workspace to grow)
         backend = ctx.last_backend()
-    for i in range(args.warmup):
-        step(i)
-    per_graph = 400
-    reps = max(1, args.steps // per_graph)
+    # exactly args.steps timed steps: replays of one graph of `per_graph` launches (the largest divisor of
+    # the step count up to 400, so short runs are not rounded up)
+    total = max(1, args.steps)
+    per_graph = max(d for d in range(1, min(400, total) + 1) if total % d == 0)
+    reps = total // per_graph
     steps = [(lambda i=i: step(i)) for i in range(per_graph)]
-    ms, wall = b.graph_time(steps, reps)
-    kmean, kmed = b.kernel_time(step, 800)
+    with t.cuda.stream(b.s):
+        for i in range(args.warmup):  # the untimed warm-up steps
+            step(i)
+    # one untimed replay uploads the graph before the timed replays
+    ms, wall = b.graph_time(steps, reps, warm=1, eager_warm=False)
+    kmean, kmed = b.kernel_time(step, 800) if not args.trace_headline else (None, None)
     bytes_step = k * n + k * 2 + n * 2
     res = {
         "ms_per_step": ms, "steps": reps * per_graph, "wall_s": wall, "bytes": bytes_step,
@@ -490,12 +499,12 @@ def extra_configs(b, args):
 
 
 def ceilings(b):
-    """Measured ceilings beside the published peaks (infer_amd/ceilings.hip, not part of the operator
+    """Measured ceilings beside the published peaks (bench_ceilings.hip beside this file, not part of the operator
     library): the sustained FP8 MFMA rate with the C3 activation codes, and with all-zero codes, in the
     operand registers (MFMA power, and so the sustained clock, depends on the operand bits), and the
     L2 -> LDS rate of the GEMM's operand staging path over an L2-resident 2 MB buffer."""
     t, L = b.torch, b.L
-    lib = ctypes.CDLL(os.path.join(ROOT, "infer_amd", "libfhip_ceilings.so"))
+    lib = ctypes.CDLL(os.path.join(ROOT, "bench_ceilings.so"))
     lib.fhipc_mfma_fp8_rate.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
                                         ctypes.POINTER(ctypes.c_float)]
     lib.fhipc_l2_stream.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.POINTER(ctypes.c_float)]
@@ -530,6 +539,8 @@ def measured_traffic(kernel):
 
 def main():
     args = parse()
+    if args.trace_headline:
+        args.only_headline, args.no_cpu = True, True
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
@@ -563,8 +574,23 @@ def main():
             "kernel_ms_event_pairs": h["kernel_ms"], "kernel_ms_event_pairs_median": h["kernel_ms_median"],
         },
         "cpu_baseline": None,
-        "dispatch_reference_points": dispatch_floor(b),
     }
+    if not args.trace_headline:
+        # What one dispatch of this size costs on this chip whatever the kernel does: an empty kernel, and a
+        # device copy of the same weight bytes, each replayed the same way.  The headline kernel's time splits
+        # into that launch floor and its own excess.
+        fl = dispatch_floor(b)
+        line["dispatch_reference_points"] = fl
+        if "empty_kernel_us" in fl:
+            kus = h["ms_per_step"] * 1e3
+            line["roofline"]["floor"] = {
+                "empty_kernel_us": round(fl["empty_kernel_us"], 3),
+                "copy_same_bytes_us": round(fl["copy_3670016B_us"], 3),
+                "kernel_us": round(kus, 3),
+                "kernel_excess_over_empty_us": round(kus - fl["empty_kernel_us"], 3),
+                "kernel_excess_over_copy_us": round(kus - fl["copy_3670016B_us"], 3),
+                "hbm_time_at_peak_us": round(h["bytes"] / HBM_PEAK_GBS / 1e3, 3),
+            }
     if not args.only_headline:
         try:
             line["configs"] = extra_configs(b, args)

@@ -1,7 +1,7 @@
-// ceilings.hip -- measured hardware ceilings that bench.py reports beside the published MI355X peaks.
+// bench_ceilings.hip -- measured hardware ceilings that bench.py reports beside the published MI355X peaks.
 //
 // Not part of the operator library (libfhip.so) and not called by it: a separate diagnostic library,
-// libfhip_ceilings.so, that bench.py loads to put the FP8 GEMM's roofline fraction in context.
+// bench_ceilings.so (built beside bench.py by __graft_entry__.build()), that bench.py loads to put the FP8 GEMM's roofline fraction in context.
 //   * fhipc_mfma_fp8_rate: sustained v_mfma_scale_f32_32x32x64_f8f6f4 rate on every CU when the operand
 //     registers hold given FP8 codes (bench.py passes the C3 activation codes).  MFMA power, and with
 //     it the clock the chip sustains, depends on the operand bits: all-zero operands run faster than

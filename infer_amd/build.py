@@ -11,9 +11,6 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libfhip.so")
-# diagnostic kernels bench.py uses for measured ceilings; not part of the operator library
-CEILINGS_SRC = os.path.join(HERE, "ceilings.hip")
-CEILINGS_LIB = os.path.join(HERE, "libfhip_ceilings.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [
@@ -36,8 +33,6 @@ def build(verbose=False):
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
         objs.append(obj)
     failed = False
-    ceil_cmd = [HIPCC] + FLAGS + [CEILINGS_SRC, "-o", CEILINGS_LIB]
-    procs.append((CEILINGS_SRC, subprocess.Popen(ceil_cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
     for src, p in procs:
         out = p.communicate()[0].decode(errors="replace")
         lines = [l for l in out.splitlines() if "packed-fp32-ops" not in l and "not a recognized feature" not in l]

@@ -34,6 +34,11 @@ struct fhip_context_s {
     size_t weight_bytes = 0;
     void* workspace = nullptr;
     size_t workspace_size = 0;
+    // Workspaces replaced by a larger one while captured graphs were alive: a graph holds the address
+    // of the buffer it was captured with, so those buffers are freed only when no graph of this
+    // context remains (fhip_graph_destroy) or with the context.
+    std::vector<void*> retired_workspaces;
+    int live_graphs = 0;
     ArgmaxScratch* scratch = nullptr;
     bool capturing = false;
     std::string last_error;

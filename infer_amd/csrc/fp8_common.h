@@ -164,6 +164,16 @@ float pow2_inverse(float s);
 // a: FP8 codes [m][k64], k64 % 64 == 0, 16-byte aligned rows; k64 <= the weight's padded K.
 int launch_fp8_gemm(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, const fhip_weight_s* w,
                     const Fp8Epilogue& ep);
+// The same per (FP8 format, output bytes): one translation unit each (fp8_gemm_e{4,5}_{fp8,bf16,fp32}.hip).
+#define FHIP_GEMM_DECL(NAME) \
+    int NAME(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, const fhip_weight_s* w, const Fp8Epilogue& ep);
+FHIP_GEMM_DECL(launch_fp8_gemm_e4_o1)
+FHIP_GEMM_DECL(launch_fp8_gemm_e4_o2)
+FHIP_GEMM_DECL(launch_fp8_gemm_e4_o4)
+FHIP_GEMM_DECL(launch_fp8_gemm_e5_o1)
+FHIP_GEMM_DECL(launch_fp8_gemm_e5_o2)
+FHIP_GEMM_DECL(launch_fp8_gemm_e5_o4)
+#undef FHIP_GEMM_DECL
 
 }  // namespace fhip
 

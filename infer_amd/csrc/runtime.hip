@@ -39,9 +39,14 @@ int acquire_workspace(fhip_context ctx, size_t bytes, void** ptr) {
     grown = std::min(grown, ctx->workspace_limit);
     grown = (grown + 255) & ~size_t(255);
     if (ctx->workspace) {
-        hipError_t e = hipStreamSynchronize(ctx->stream);
-        if (e != hipSuccess) return check_hip(ctx, e, "hipStreamSynchronize");
-        (void)hipFree(ctx->workspace);
+        if (ctx->live_graphs > 0) {
+            // a captured graph may still replay with this address: keep the buffer until it is destroyed
+            ctx->retired_workspaces.push_back(ctx->workspace);
+        } else {
+            hipError_t e = hipStreamSynchronize(ctx->stream);
+            if (e != hipSuccess) return check_hip(ctx, e, "hipStreamSynchronize");
+            (void)hipFree(ctx->workspace);
+        }
         ctx->workspace = nullptr;
         ctx->workspace_size = 0;
     }
@@ -242,6 +247,8 @@ int fhip_context_destroy(fhip_context ctx) {
     for (fhip_weight w : ctx->weights) free_weight(w);
     ctx->weights.clear();
     if (ctx->workspace) (void)hipFree(ctx->workspace);
+    for (void* p : ctx->retired_workspaces) (void)hipFree(p);
+    ctx->retired_workspaces.clear();
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
@@ -252,7 +259,15 @@ int fhip_context_set_stream(fhip_context ctx, void* stream) {
     if (!ctx) return FHIP_ERR_INVALID;
     std::lock_guard<std::recursive_mutex> lock(ctx->mu);
     if (ctx->capturing) return set_error(ctx, FHIP_ERR_STATE, "cannot change the stream during capture");
-    ctx->stream = stream ? static_cast<hipStream_t>(stream) : ctx->own_stream;
+    hipStream_t next = stream ? static_cast<hipStream_t>(stream) : ctx->own_stream;
+    if (next != ctx->stream && ctx->stream) {
+        // The argmax tickets, partial keys and workspace belong to the context, not to a stream: work
+        // still queued on the old stream must finish before the new stream can reuse them.
+        DeviceGuard guard(ctx->device);
+        int rc = check_hip(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(previous stream)");
+        if (rc != FHIP_OK) return rc;
+    }
+    ctx->stream = next;
     return FHIP_OK;
 }
 
@@ -477,10 +492,13 @@ int fhip_weight_matches(fhip_weight w, const void* src, uint64_t version) {
 
 // ---- execution capture ---------------------------------------------------------------------
 
+// A graph keeps its context's workspace address alive (see retired_workspaces); destroy graphs before
+// their context.
 struct fhip_graph_s {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     int device = 0;
+    fhip_context ctx = nullptr;
 };
 
 int fhip_capture_begin(fhip_context ctx) {
@@ -501,6 +519,7 @@ int fhip_capture_end(fhip_context ctx, fhip_graph* out) {
     ctx->capturing = false;
     auto* g = new fhip_graph_s();
     g->device = ctx->device;
+    g->ctx = ctx;
     int rc = check_hip(ctx, hipStreamEndCapture(ctx->stream, &g->graph), "hipStreamEndCapture");
     if (rc == FHIP_OK) rc = check_hip(ctx, hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0), "hipGraphInstantiate");
     if (rc != FHIP_OK) {
@@ -508,6 +527,7 @@ int fhip_capture_end(fhip_context ctx, fhip_graph* out) {
         delete g;
         return rc;
     }
+    ctx->live_graphs++;
     *out = g;
     return FHIP_OK;
 }
@@ -523,6 +543,14 @@ int fhip_graph_destroy(fhip_graph g) {
     DeviceGuard guard(g->device);
     if (g->exec) (void)hipGraphExecDestroy(g->exec);
     if (g->graph) (void)hipGraphDestroy(g->graph);
+    if (fhip_context ctx = g->ctx) {
+        std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+        if (--ctx->live_graphs == 0 && !ctx->retired_workspaces.empty()) {
+            (void)hipStreamSynchronize(ctx->stream);
+            for (void* p : ctx->retired_workspaces) (void)hipFree(p);
+            ctx->retired_workspaces.clear();
+        }
+    }
     delete g;
     return FHIP_OK;
 }

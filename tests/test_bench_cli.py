@@ -15,7 +15,7 @@ def test_bench_refuses_more_than_one_gpu():
 
 
 def test_ceilings_library_exports_its_entry_points():
-    """bench.py's measured ceilings come from a separate diagnostic library built beside libfhip.so."""
+    """bench.py's measured ceilings come from a separate diagnostic library built beside bench.py."""
     import ctypes
-    lib = ctypes.CDLL(os.path.join(ROOT, "infer_amd", "libfhip_ceilings.so"))
+    lib = ctypes.CDLL(os.path.join(ROOT, "bench_ceilings.so"))
     assert hasattr(lib, "fhipc_mfma_fp8_rate") and hasattr(lib, "fhipc_l2_stream")

@@ -4,7 +4,8 @@ Oracle: src/kernel/common/qwen_gemm_argmax.cc:28-49 restated in oracle/feather_o
 Rule (the accumulation order differs from the oracle's K-ordered fp32 sum): the token must match
 exactly; a differing token is accepted only as an "order-induced BF16 boundary flip", i.e. the
 oracle's BF16 values of both candidates are tied or adjacent and their fp32 sums differ by no more
-than K * 2^-24 * sum_k |a_k * w_k| -- and such flips are counted and printed.
+than K * 2^-24 * sum_k |a_k * w_k| -- and such flips are counted and printed.  On the seeded
+BASELINE config-5 inputs no flip is allowed: the tokens must equal the oracle's.
 """
 import numpy as np
 import pytest
@@ -46,6 +47,11 @@ def check_tokens(a, w, got, logits_got=None):
     return flips
 
 
+# Order flips the seeded C5 inputs are allowed to show: (m, row) -> (oracle token, HIP token).  Empty:
+# on the BASELINE config-5 inputs every row's token must equal the oracle's exactly.
+C5_KNOWN_FLIPS = {}
+
+
 @pytest.mark.parametrize("m", [1, 8])
 def test_bf16_argmax_config5(ctx, m):
     k, v = 1024, 151936
@@ -54,14 +60,17 @@ def test_bf16_argmax_config5(ctx, m):
     logits = torch.empty((m, v), dtype=torch.float32, device="cuda")
     ctx.bf16_gemv_argmax(dev(a), dev(w), tokens, logits)
     got = tokens.cpu().numpy()
-    flips = check_tokens(a, w, got)
-    print(f"m={m} tokens {got.tolist()} order flips {flips}")
-    assert flips <= max(1, m // 4)
-    # logits within tolerance of the oracle's fp32 sums
+    lg = logits.cpu().numpy()
     for j in range(m):
-        _, ref = po.bf16_gemm_argmax(a[j], w, want_logits=True)
-        lg = logits.cpu().numpy()[j]
-        assert np.max(np.abs(lg - ref)) <= 1e-2 * np.max(np.abs(ref))
+        tok, ref = po.bf16_gemm_argmax(a[j], w, want_logits=True)
+        print(f"m={m} row {j}: token {int(got[j])} oracle {tok} logit {ref[tok]!r}")
+        if (m, j) in C5_KNOWN_FLIPS:
+            assert (tok, int(got[j])) == C5_KNOWN_FLIPS[(m, j)]
+        else:
+            assert got[j] == tok, (f"row {j}: token {int(got[j])} (oracle logit {ref[int(got[j])]!r}) vs oracle "
+                                   f"{tok} (oracle logit {ref[tok]!r})")
+        # logits within tolerance of the oracle's fp32 sums
+        assert np.max(np.abs(lg[j] - ref)) <= 1e-2 * np.max(np.abs(ref))
 
 
 @pytest.mark.parametrize("m", [1, 3])
@@ -134,15 +143,27 @@ def test_fp8_argmax_head(ctx, dtype, m, k):
     s_out = fp8_pow2_scale(float(np.abs(sums).max()), dtype)
     tokens = torch.empty(m, dtype=torch.int64, device="cuda")
     ctx.fp8_gemv_argmax(dtype, dev(a_codes), sa, dev(w_codes), sw, s_out, tokens)
-    vals_all = po.cast_from_fp8(dtype, po.fp8_gemm(dtype, a_codes, sa, w_codes, sw, True, s_out), s_out, po.FP32)
+    abs_sums = po.fp8_sums(dtype, a_codes & 0x7F, sa, w_codes & 0x7F, sw, True)
+    dec = po.fp8_decode_table(dtype).astype(np.float64)
+
+    def value(x):  # the head's selection value of an fp32 sum: Dec(Enc(x / s_out)) (x86/linear_fp8.cc:757-788)
+        return dec[po.fp8_encode(dtype, np.asarray([x / s_out], np.float32))[0]]
+
     for j in range(m):
         ref = po.fp8_gemm_argmax(dtype, a_codes[j], sa, w_codes, sw, s_out)
         got = int(tokens[j].item())
-        if got != ref:
-            # FP8 output quantization creates many ties; accept only an equal-valued earlier/later candidate
-            # whose sums straddle an FP8 code boundary by accumulation-order rounding.
-            vals = vals_all[j]
-            assert abs(vals[got] - vals[ref]) <= abs(vals[ref]) * 0.13, (j, got, ref)
+        if got == ref:
+            continue
+        # Summation-order flip only: both fp32 sums may move by the recursive-summation bound of either order,
+        # E = 2 * K * 2^-24 * sum_k |a_k w_k|.  The HIP token must then be able to win: its largest reachable
+        # FP8 value must reach the oracle token's smallest one (and on equal values come first).
+        e_got = 2.0 * k * 2.0 ** -24 * abs_sums[j, got]
+        e_ref = 2.0 * k * 2.0 ** -24 * abs_sums[j, ref]
+        hi_got = value(sums[j, got] + e_got)
+        lo_ref = value(sums[j, ref] - e_ref)
+        print(f"row {j}: token {got} (sum {sums[j, got]!r}) vs oracle {ref} (sum {sums[j, ref]!r}), "
+              f"bounds {e_got:.3g} / {e_ref:.3g}")
+        assert hi_got > lo_ref or (hi_got == lo_ref and got < ref), (j, got, ref)
 
 
 def test_argmax_two_contexts_concurrent():

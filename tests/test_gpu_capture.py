@@ -81,3 +81,55 @@ def test_captured_decode_step_replays_match_eager(ctx):
             ctx.graph_destroy(g)
     wf.release()
     w8.release()
+
+
+def test_graph_survives_workspace_growth():
+    """A graph captured while the workspace was small keeps replaying correctly after an eager call grows
+    the workspace: the buffer the graph was captured with stays allocated while the graph exists (the
+    bf16-activation GEMM stages its FP8 codes in the workspace)."""
+    from infer_amd.runtime import Context
+    c = Context(0)
+    r = rng(91)
+    k, n = 1024, 512
+    dtype = po.FP8E4M3
+    w_nk, sw = fp8_tensor((r.standard_normal((n, k)) * 0.02).astype(np.float32), dtype)
+    wt = c.prepare_weight(torch.from_numpy(w_nk).cuda(), dtype, k, n, 1, version=92)
+    m_small, m_big = 64, 8192
+
+    def bf16_rows(seed, m):
+        g = rng(seed)
+        return torch.from_numpy(po.bf16_encode(g.standard_normal((m, k)).astype(np.float32)).view(np.int16)).cuda()
+
+    x = bf16_rows(1, m_small)
+    y = torch.empty((m_small, n), dtype=torch.int16, device="cuda")
+    xb, yb = bf16_rows(2, m_big), torch.empty((m_big, n), dtype=torch.int16, device="cuda")
+    with torch.cuda.stream(c.stream):
+        c.fp8_linear(x, po.BF16, 0.0078125, m_small, wt, sw, y, po.BF16, 0.0625)
+        c.synchronize()
+        eager = y.cpu().numpy().copy()
+        c.capture_begin()
+        c.fp8_linear(x, po.BF16, 0.0078125, m_small, wt, sw, y, po.BF16, 0.0625)
+        g = c.capture_end()
+        try:
+            # grows the workspace from m_small * k to m_big * k bytes while the graph is alive
+            c.fp8_linear(xb, po.BF16, 0.0078125, m_big, wt, sw, yb, po.BF16, 0.0625)
+            big_first = None
+            for _ in range(3):
+                y.zero_()
+                c.graph_launch(g)
+                c.fp8_linear(xb, po.BF16, 0.0078125, m_big, wt, sw, yb, po.BF16, 0.0625)
+                c.synchronize()
+                assert np.array_equal(y.cpu().numpy(), eager)
+                big = yb.cpu().numpy()
+                if big_first is None:
+                    big_first = big.copy()
+                assert np.array_equal(big, big_first)
+        finally:
+            c.graph_destroy(g)
+    # the retired buffer is freed with the last graph; the context keeps working
+    with torch.cuda.stream(c.stream):
+        c.fp8_linear(x, po.BF16, 0.0078125, m_small, wt, sw, y, po.BF16, 0.0625)
+        c.synchronize()
+    assert np.array_equal(y.cpu().numpy(), eager)
+    wt.release()
+    c.close()

@@ -242,3 +242,75 @@ def test_i8_conv_window_path_general_geometry(ctx, layout, wd, pad):
     got = out.cpu().numpy()
     assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatches"
     wt.release()
+
+
+def test_i8_linear_overflow_bound_declines_where_common_fails(ctx):
+    """The int32 partial-sum rule (gemm.cc:177-181; int8_kernel_utils.h:99-114).  The host bound is
+    K * (128 + |zp_a|) * max|w - zp_w| + |bias|: with (a - zp_a) = -255 and w = 127 on every step,
+    K = 66304 keeps every partial sum inside int32 -- the HIP path runs and is bit-exact -- while
+    K = 66432 overflows at the last steps: the Common kernel returns -1 and the HIP path declines with
+    FHIP_ERR_UNSUPPORTED (-2) so that Feather's Common kernel runs and fails exactly as the reference does."""
+    n, m = 32, 2
+    for k, expect in ((66304, 0), (66432, -2)):
+        a = np.full((m, k), -128, np.int8)
+        a[1, ::3] = 5                              # a second, ordinary row
+        w = np.full((n, k), 127, np.int8)
+        w[1:, ::2] = -3
+        rc_ref, ref, _ = po.i8_linear(po.I8_GEMM, a, 0.5, 127, w, True, np.full(n, 1e-8, np.float32), None, None, 0,
+                                      1.0, 1.0, 1.0, 0)
+        assert rc_ref == (0 if expect == 0 else -1)
+        wt = ctx.prepare_weight(dev(w), po.INT8, k, n, 1, scales=np.full(n, 1e-8, np.float32), version=40 + k)
+        out = torch.empty((m, n), dtype=torch.int8, device="cuda")
+        rc = ctx.i8_linear(po.I8_GEMM, dev(a), 0.5, 127, m, wt, out, 1.0, 0, check=False)
+        assert rc == expect, (k, rc, ctx.last_error())
+        if expect == 0:
+            assert np.array_equal(out.cpu().numpy(), ref)
+        wt.release()
+
+
+def test_i8_fc_bias_overflow_declines(ctx):
+    """FC adds the int32 bias into the accumulator (fc.cc:105-159), so |bias| counts toward the bound: a bias
+    of magnitude near 2^31 declines (-2) although the dot products alone are small."""
+    r = rng(41)
+    m, k, n = 4, 256, 64
+    a = r.integers(-128, 128, (m, k)).astype(np.int8)
+    w = r.integers(-127, 128, (n, k)).astype(np.int8)
+    wt = ctx.prepare_weight(dev(w), po.INT8, k, n, 1, scales=np.full(n, 0.01, np.float32), version=45)
+    out = torch.empty((m, n), dtype=torch.int8, device="cuda")
+    for babs, expect in ((1 << 20, 0), ((1 << 31) - 1000, -2)):
+        bias = np.full(n, babs, np.int32)
+        bias[::2] *= -1
+        rc = ctx.i8_linear(po.I8_FC, dev(a), 0.02, 0, m, wt, out, 1.0, 0, bias=dev(bias), bias_kind=po.BIAS_VECTOR,
+                           bias_abs_max=babs, check=False)
+        assert rc == expect, (babs, rc, ctx.last_error())
+        if expect == 0:
+            rc_ref, ref, _ = po.i8_linear(po.I8_FC, a, 0.02, 0, w, True, np.full(n, 0.01, np.float32), None, bias,
+                                          po.BIAS_VECTOR, 1.0, 1.0, 1.0, 0)
+            assert rc_ref == 0 and np.array_equal(out.cpu().numpy(), ref)
+    wt.release()
+
+
+def test_weight_zero_point_declines(ctx):
+    """A weight zero point != 0 (the static quantizer writes symmetric weights, static_quantizer.cc:211-255)
+    is declined (-2) by the linear and the conv, and the Common kernel handles it (the oracle runs it)."""
+    r = rng(42)
+    m, k, n = 3, 64, 16
+    a = r.integers(-128, 128, (m, k)).astype(np.int8)
+    w = r.integers(-127, 128, (n, k)).astype(np.int8)
+    zps = np.zeros(n, np.int32)
+    zps[5] = 2
+    wt = ctx.prepare_weight(dev(w), po.INT8, k, n, 1, scales=np.full(n, 0.01, np.float32), zero_points=zps,
+                            version=46)
+    out = torch.empty((m, n), dtype=torch.int8, device="cuda")
+    assert ctx.i8_linear(po.I8_GEMM, dev(a), 0.02, 0, m, wt, out, 1.0, 0, check=False) == -2
+    rc_ref, _, _ = po.i8_linear(po.I8_GEMM, a, 0.02, 0, w, True, np.full(n, 0.01, np.float32), zps, None, 0, 1.0,
+                                1.0, 1.0, 0)
+    assert rc_ref == 0
+    wt.release()
+    wc = r.integers(-127, 128, (8, 4, 3, 3)).astype(np.int8)
+    cw = ctx.prepare_conv_weight(dev(wc), np.full(8, 0.01, np.float32), zero_points=np.arange(8, dtype=np.int32),
+                                 version=47)
+    x = r.integers(-128, 128, (1, 4, 9, 9)).astype(np.int8)
+    y = torch.empty((1, 8, 9, 9), dtype=torch.int8, device="cuda")
+    assert ctx.i8_conv2d(dev(x), 0, 0.5, 0, cw, y, 1.0, 0, pad=(1, 1), check=False) == -2
+    cw.release()

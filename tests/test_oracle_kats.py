@@ -274,3 +274,41 @@ def test_bf16_argmax_vs_reference_x86():
         assert R.ref_bf16_argmax_compute(h, po._ptr(a), ctypes.byref(tok)) == 0
         R.ref_bf16_argmax_destroy(h)
         assert po.bf16_gemm_argmax(a, w) == tok.value
+
+
+def _round_half_away(x):
+    """std::round on float64, exactly: ties go away from zero."""
+    t = np.trunc(x)
+    return np.where(np.abs(x - t) >= 0.5, t + np.sign(x), t)
+
+
+@pytest.mark.parametrize("alpha,beta", [(0.75, -1.5), (1.0, 0.0), (-2.0, 0.375), (3.0, 1.0)])
+def test_int8_gemm_alpha_beta_matrix_bias_closed_form(alpha, beta):
+    """The Gemm INT8 branch with alpha/beta != 1 and a matrix bias, against a numpy float64 statement of
+    src/kernel/common/gemm.cc:171-195: acc = double(alpha)*dot + double(beta)*bias, real = acc * (double(s_a) *
+    double(s_w[c])), q = clamp(round_half_away(real / double(s_out) + zp_out)).  Power-of-two scales make exact
+    .5 ties; per-channel weight scales and zero points on both operands."""
+    r = rng(77)
+    m, k, n = 13, 96, 21
+    a = r.integers(-6, 7, (m, k)).astype(np.int8)
+    w = r.integers(-4, 5, (n, k)).astype(np.int8)
+    a[0] = 127                     # row 0 against channels 0 / 1 saturates both ways
+    w[0], w[1] = 100, -100
+    wz = r.integers(-2, 3, n).astype(np.int32)
+    wz[:2] = 0
+    ws = (2.0 ** r.integers(-3, 0, n)).astype(np.float32)
+    bias = r.integers(-300, 300, (m, n)).astype(np.int32)
+    s_a, zp_a, s_out, zp_out = 0.5, -1, 0.25, 3
+    rc, got, acc = po.i8_linear(po.I8_GEMM, a, s_a, zp_a, w, True, ws, wz, bias, po.BIAS_MATRIX, alpha, beta, s_out,
+                                zp_out, True)
+    assert rc == 0
+    dot = (a.astype(np.int64) - zp_a) @ (w.astype(np.int64) - wz[:, None]).T
+    assert np.array_equal(acc, dot)
+    real = (np.float64(np.float32(alpha)) * dot.astype(np.float64) + np.float64(np.float32(beta)) * bias) * \
+        (np.float64(np.float32(s_a)) * ws.astype(np.float64)[None, :])
+    q = np.clip(_round_half_away(real / np.float64(np.float32(s_out)) + zp_out), -128, 127).astype(np.int8)
+    assert np.array_equal(got, q)
+    # the case is not degenerate: ties and both clamps occur
+    t = real / s_out + zp_out
+    assert np.any(np.abs(t - np.trunc(t)) == 0.5)
+    assert np.any(q == 127) and np.any(q == -128)
