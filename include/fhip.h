@@ -172,6 +172,17 @@ int fhip_dequantize_linear(fhip_context ctx, const int8_t* src, int64_t count, i
  * logits (optional, [m, v] fp32) receives the fp32 sums. */
 int fhip_bf16_gemv_argmax(fhip_context ctx, const uint16_t* a, int64_t m, int64_t k, const uint16_t* w, int64_t v,
                           int64_t* tokens, float* logits);
+/* No counterpart in the reference.  For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the same computation
+ * and results as fhip_bf16_gemv_argmax, but the kernels' ticket counters and per-block partial
+ * keys live in a static device array of 128 KiB per GPU (set up once per device by
+ * fhip_context_create) instead of the context's workspace, so the call allocates nothing.
+ * Returns FHIP_ERR_UNSUPPORTED when the vocabulary needs more partial keys than the array holds
+ * (not the case up to 2 blocks per CU on 480 CUs).  Every context on one GPU shares the array:
+ * calls that overlap on one GPU (two streams, two contexts, two host threads) race and must be
+ * ordered by the caller.  Each call clears the counters with a kernel before it starts. */
+int fhip_bf16_gemv_argmax_noalloc(fhip_context ctx, const uint16_t* a, int64_t m, int64_t k, const uint16_t* w,
+                                  int64_t v, int64_t* tokens, float* logits);
 /* FP8 head: Gemm(transB) with out_scale, Cast(fp8 -> bf16), greedy selection
  * (x86/linear_fp8.cc:733-1004; qwen_gemm_argmax_fusion_pass.cc:142-181). */
 int fhip_fp8_gemv_argmax(fhip_context ctx, int dtype, const uint8_t* a, float a_scale, int64_t m, int64_t k,

@@ -53,6 +53,7 @@ SIGNATURES = {
     "fhip_quantize_linear": (_INT, [_P, _INT, _P, _I64, _I64, _I64, _P, _P, _I64, _P]),
     "fhip_dequantize_linear": (_INT, [_P, _P, _I64, _I64, _I64, _P, _P, _I64, _INT, _P]),
     "fhip_bf16_gemv_argmax": (_INT, [_P, _P, _I64, _I64, _P, _I64, _P, _P]),
+    "fhip_bf16_gemv_argmax_noalloc": (_INT, [_P, _P, _I64, _I64, _P, _I64, _P, _P]),
     "fhip_fp8_gemv_argmax": (_INT, [_P, _INT, _P, _F, _I64, _I64, _P, _F, _I64, _F, _P]),
     "fhip_capture_begin": (_INT, [_P]),
     "fhip_capture_end": (_INT, [_P, _PP]),

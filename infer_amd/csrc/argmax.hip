@@ -19,6 +19,8 @@
 #include "fhip_internal.h"
 #include "codec.h"
 
+#include <algorithm>
+
 namespace {
 
 typedef float v2f __attribute__((ext_vector_type(2)));
@@ -421,40 +423,45 @@ __global__ __launch_bounds__(kThreads) void gemv_argmax_mfma_kernel(const uint8_
     ticket_and_finish<16>(partials, m, scratch, tokens);
 }
 
-template <int KIND>
-int launch(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k, const uint8_t* w, int64_t v, HeadParams hp,
-           int64_t* tokens, const char* name) {
+// Grid and partial-key workspace of one call.  The grid strides over the vocabulary; measured on the C5
+// head: the MFMA kernel (m >= 2) is fastest with 2 blocks per CU (1, 3, 4: 79, 68, 77 us against 62),
+// the m = 1 kernel with 1 (54.2 against 55.1 us).  The workspace is sized for either kernel's grid, so a
+// later call with other rows does not need a bigger one (e.g. under capture).
+struct Plan {
+    int64_t grid1;      // blocks of the m = 1 kernel
+    int64_t mgrid;      // blocks of the MFMA kernel
+    size_t ws_bytes;    // partial keys: 16 per block
+};
+
+Plan plan_for(int device, int64_t v) {
     int dev_cus = 256;
-    (void)hipDeviceGetAttribute(&dev_cus, hipDeviceAttributeMultiprocessorCount, ctx->device);
+    (void)hipDeviceGetAttribute(&dev_cus, hipDeviceAttributeMultiprocessorCount, device);
     const int64_t rows_per_block = (int64_t)kWaves * kRows;
-    int64_t grid = (v + rows_per_block - 1) / rows_per_block;
-    // grid-stride over the vocabulary; measured on the C5 head: the MFMA kernel (m >= 2) is fastest with 2
-    // blocks per CU (1, 3, 4: 79, 68, 77 us against 62), the m = 1 kernel with 1 (54.2 against 55.1 us)
     const int64_t cap = (int64_t)dev_cus * 2;
-    const int64_t cap1 = (int64_t)dev_cus;
-    if (grid > cap1) grid = cap1;
-    // per-block partial keys of either kernel (sized for the larger grid, so a later call with other rows
-    // does not need a bigger workspace, e.g. under capture)
-    int64_t ws_blocks = (v + 15) / 16;
-    if (ws_blocks > cap) ws_blocks = cap;
-    if (ws_blocks < grid) ws_blocks = grid;
-    void* ws = nullptr;
-    int rc = fhip::acquire_workspace(ctx, (size_t)ws_blocks * 16 * sizeof(unsigned long long), &ws);
-    if (rc != FHIP_OK) return rc;
-    auto* partials = static_cast<unsigned long long*>(ws);
+    Plan p;
+    p.grid1 = std::min<int64_t>((v + rows_per_block - 1) / rows_per_block, dev_cus);
+    p.mgrid = std::min<int64_t>((v + 15) / 16, cap);
+    const int64_t ws_blocks = std::max(p.mgrid, p.grid1);
+    p.ws_bytes = (size_t)ws_blocks * 16 * sizeof(unsigned long long);
+    return p;
+}
+
+// Enqueues the kernel for (m, k) on `stream`.  Returns FHIP_OK, FHIP_ERR_UNSUPPORTED (m > 16) or the
+// launch error as FHIP_ERR_HIP (with *err set).
+template <int KIND>
+int launch_on(hipStream_t stream, const Plan& plan, const uint8_t* a, int64_t m, int64_t k, const uint8_t* w,
+              int64_t v, HeadParams hp, unsigned long long* partials, ArgmaxScratch* tickets, int64_t* tokens,
+              hipError_t* err) {
     const int64_t bytes = k * (KIND == 0 ? 2 : 1);
     if (m >= 2) {
         const int64_t step_bytes = KIND == 0 ? 64 : 128;
         const int64_t spw_need = ((bytes + step_bytes - 1) / step_bytes + kWaves - 1) / kWaves;
-        int64_t mgrid = (v + 15) / 16;
-        if (mgrid > cap) mgrid = cap;
-#define FHIP_ARGMAX_MFMA_CASE(SPW)                                                                                  \
-        if (spw_need <= (SPW)) {                                                                                    \
-            gemv_argmax_mfma_kernel<KIND, SPW><<<(unsigned)mgrid, kThreads, 0, ctx->stream>>>(a, m, k, w, v, hp,    \
-                                                                                   partials, ctx->scratch, tokens); \
-            ctx->last_backend = name;                                                                               \
-            FHIP_CHECK_LAUNCH(ctx, "gemv_argmax_mfma_kernel");                                                      \
-            return FHIP_OK;                                                                                         \
+#define FHIP_ARGMAX_MFMA_CASE(SPW)                                                                              \
+        if (spw_need <= (SPW)) {                                                                                \
+            gemv_argmax_mfma_kernel<KIND, SPW><<<(unsigned)plan.mgrid, kThreads, 0, stream>>>(a, m, k, w, v, hp, \
+                                                                                 partials, tickets, tokens);    \
+            *err = hipGetLastError();                                                                           \
+            return *err == hipSuccess ? FHIP_OK : FHIP_ERR_HIP;                                                 \
         }
         FHIP_ARGMAX_MFMA_CASE(2)
         FHIP_ARGMAX_MFMA_CASE(4)
@@ -463,19 +470,119 @@ int launch(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k, const uint8
 #undef FHIP_ARGMAX_MFMA_CASE
     }
     const int t = bytes <= 1024 ? 1 : (bytes <= 2048 ? 2 : 4);
-#define FHIP_ARGMAX_CASE(MT, T)                                                                                   \
-    if (m <= MT && t == T) {                                                                                      \
-        gemv_argmax_kernel<KIND, MT, T><<<(unsigned)grid, kThreads, 0, ctx->stream>>>(a, m, k, w, v, hp, partials, \
-                                                                                      ctx->scratch, tokens);     \
-        ctx->last_backend = name;                                                                                 \
-        FHIP_CHECK_LAUNCH(ctx, "gemv_argmax_kernel");                                                             \
-        return FHIP_OK;                                                                                           \
+#define FHIP_ARGMAX_CASE(MT, T)                                                                              \
+    if (m <= MT && t == T) {                                                                                 \
+        gemv_argmax_kernel<KIND, MT, T><<<(unsigned)plan.grid1, kThreads, 0, stream>>>(a, m, k, w, v, hp,    \
+                                                                                   partials, tickets, tokens); \
+        *err = hipGetLastError();                                                                            \
+        return *err == hipSuccess ? FHIP_OK : FHIP_ERR_HIP;                                                  \
     }
     FHIP_ARGMAX_CASE(1, 1)
     FHIP_ARGMAX_CASE(1, 2)
     FHIP_ARGMAX_CASE(1, 4)
 #undef FHIP_ARGMAX_CASE
-    return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "gemv_argmax: m > 16");
+    return FHIP_ERR_UNSUPPORTED;
+}
+
+template <int KIND>
+int launch(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k, const uint8_t* w, int64_t v, HeadParams hp,
+           int64_t* tokens, const char* name) {
+    const Plan plan = plan_for(ctx->device, v);
+    void* ws = nullptr;
+    int rc = fhip::acquire_workspace(ctx, plan.ws_bytes, &ws);
+    if (rc != FHIP_OK) return rc;
+    hipError_t err = hipSuccess;
+    rc = launch_on<KIND>(ctx->stream, plan, a, m, k, w, v, hp, static_cast<unsigned long long*>(ws), ctx->scratch,
+                         tokens, &err);
+    if (rc == FHIP_ERR_HIP) return fhip::check_hip(ctx, err, "gemv_argmax launch");
+    if (rc != FHIP_OK) return fhip::set_error(ctx, rc, "gemv_argmax: m > 16");
+    ctx->last_backend = name;
+    return FHIP_OK;
+}
+
+// ---- the allocation-free variant -------------------------------------------------------------------
+// One array per GPU holds the ticket counters (first kNoAllocTicketBytes) and the per-block partial
+// keys.  Host code never passes `scratch` itself to a kernel: its address on each device comes from
+// hipGetSymbolAddress at context creation (noalloc_setup), kept per device in g_scratch_ptr.
+constexpr size_t kNoAllocTicketBytes = 8192;
+static_assert(sizeof(ArgmaxScratch) <= kNoAllocTicketBytes, "ticket block must fit its reserved space");
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Zeroes the ticket counters with an ordinary kernel (a memset node would misbehave under graph capture).
+__global__ void clear_tickets_kernel(unsigned int* t, int words) {
+    for (int i = threadIdx.x; i < words; i += blockDim.x) t[i] = 0u;
+}
+
+}  // namespace
+
+namespace fhip {
+
+int noalloc_setup(fhip_context ctx) {
+    if (ctx->device < 0 || ctx->device >= kMaxDevices)
+        return set_error(ctx, FHIP_ERR_UNSUPPORTED, "device index beyond the scratch table");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[ctx->device]) return FHIP_OK;
+    void* ptr = nullptr;  // the caller made ctx->device current
+    int rc = check_hip(ctx, hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (rc != FHIP_OK) return rc;
+    g_scratch_ptr[ctx->device] = ptr;
+    return FHIP_OK;
+}
+
+}  // namespace fhip
+
+namespace {
+
+template <int KIND>
+int launch_noalloc(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k, const uint8_t* w, int64_t v,
+                   HeadParams hp, int64_t* tokens, const char* name) {
+    void* base = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        base = ctx->device >= 0 && ctx->device < kMaxDevices ? g_scratch_ptr[ctx->device] : nullptr;
+    }
+    if (!base) return fhip::set_error(ctx, FHIP_ERR_STATE, "no-alloc scratch was not set up for this device");
+    const Plan plan = plan_for(ctx->device, v);
+    if (kNoAllocTicketBytes + plan.ws_bytes > kNoAllocScratchBytes)
+        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED,
+                               "gemv_argmax_noalloc: " + std::to_string(kNoAllocTicketBytes + plan.ws_bytes) +
+                                   " B of scratch needed, the static scratch holds " +
+                                   std::to_string(kNoAllocScratchBytes) + " B");
+    auto* tickets = static_cast<ArgmaxScratch*>(base);
+    auto* partials = reinterpret_cast<unsigned long long*>(static_cast<unsigned char*>(base) + kNoAllocTicketBytes);
+    clear_tickets_kernel<<<1, 256, 0, ctx->stream>>>(static_cast<unsigned int*>(base),
+                                                     (int)(sizeof(ArgmaxScratch) / sizeof(unsigned int)));
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fhip::check_hip(ctx, err, "clear_tickets_kernel");
+    int rc = launch_on<KIND>(ctx->stream, plan, a, m, k, w, v, hp, partials, tickets, tokens, &err);
+    if (rc == FHIP_ERR_HIP) return fhip::check_hip(ctx, err, "gemv_argmax launch");
+    if (rc != FHIP_OK) return fhip::set_error(ctx, rc, "gemv_argmax: m > 16");
+    ctx->last_backend = name;
+    return FHIP_OK;
+}
+
+}  // namespace
+
+namespace {
+
+// Argument checks of the BF16 head (both entry points).  Returns FHIP_OK with nothing to do for m == 0.
+int check_bf16_args(fhip_context ctx, const uint16_t* a, int64_t m, int64_t k, const uint16_t* w, int64_t v,
+                    const int64_t* tokens, const char* fn) {
+    if (!ctx) return FHIP_ERR_INVALID;
+    if (m == 0) return FHIP_OK;  // no rows: nothing to select (the reference's loops run zero times)
+    if (m > 0 && (k == 0 || v == 0))
+        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, std::string(fn) + ": empty K or vocabulary");
+    if (!a || !w || !tokens || m < 0 || k < 0 || v < 0)
+        return fhip::set_error(ctx, FHIP_ERR_INVALID, std::string(fn) + ": bad arguments");
+    if (m > kArgmaxMaxRows || (k * 2) % 16 != 0 || k * 2 > 4096 || v >= (int64_t(1) << 32))
+        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, std::string(fn) + ": needs m <= 16, k % 8 == 0, k <= 2048");
+    if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(w)) & 15)
+        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, std::string(fn) + ": pointers must be 16-byte aligned");
+    return FHIP_OK;
 }
 
 }  // namespace
@@ -484,18 +591,20 @@ extern "C" {
 
 int fhip_bf16_gemv_argmax(fhip_context ctx, const uint16_t* a, int64_t m, int64_t k, const uint16_t* w, int64_t v,
                           int64_t* tokens, float* logits) {
-    if (!ctx) return FHIP_ERR_INVALID;
-    if (m == 0) return FHIP_OK;  // no rows: nothing to select (the reference's loops run zero times)
-    if (m > 0 && (k == 0 || v == 0))
-        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "bf16_gemv_argmax: empty K or vocabulary");
-    if (!a || !w || !tokens || m < 0 || k < 0 || v < 0) return fhip::set_error(ctx, FHIP_ERR_INVALID, "bf16_gemv_argmax: bad arguments");
-    if (m > kArgmaxMaxRows || (k * 2) % 16 != 0 || k * 2 > 4096 || v >= (int64_t(1) << 32))
-        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "bf16_gemv_argmax: needs m <= 16, k % 8 == 0, k <= 2048");
-    if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(w)) & 15)
-        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "bf16_gemv_argmax: pointers must be 16-byte aligned");
+    int rc = check_bf16_args(ctx, a, m, k, w, v, tokens, "bf16_gemv_argmax");
+    if (rc != FHIP_OK || m == 0) return rc;
     HeadParams hp{1.0f, 1.0f, logits};
     return launch<0>(ctx, reinterpret_cast<const uint8_t*>(a), m, k, reinterpret_cast<const uint8_t*>(w), v, hp, tokens,
                      "bf16_gemv_argmax");
+}
+
+int fhip_bf16_gemv_argmax_noalloc(fhip_context ctx, const uint16_t* a, int64_t m, int64_t k, const uint16_t* w,
+                                  int64_t v, int64_t* tokens, float* logits) {
+    int rc = check_bf16_args(ctx, a, m, k, w, v, tokens, "bf16_gemv_argmax_noalloc");
+    if (rc != FHIP_OK || m == 0) return rc;
+    HeadParams hp{1.0f, 1.0f, logits};
+    return launch_noalloc<0>(ctx, reinterpret_cast<const uint8_t*>(a), m, k, reinterpret_cast<const uint8_t*>(w), v,
+                             hp, tokens, "bf16_gemv_argmax_noalloc");
 }
 
 int fhip_fp8_gemv_argmax(fhip_context ctx, int dtype, const uint8_t* a, float a_scale, int64_t m, int64_t k,

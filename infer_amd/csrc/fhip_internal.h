@@ -23,6 +23,10 @@ struct ArgmaxScratch {
     unsigned int group_done[kTicketGroups][32];  // [g][0] is the counter
 };
 
+// Size of the static device array behind fhip_bf16_gemv_argmax_noalloc (ticket counters plus one
+// 16-key block of partial keys per workgroup; the C5 head at 2 blocks per CU on 256 CUs needs 72 KiB).
+constexpr size_t kNoAllocScratchBytes = size_t(128) << 10;
+
 struct fhip_weight_s;
 
 struct fhip_context_s {
@@ -81,6 +85,10 @@ int set_error(fhip_context ctx, int code, const std::string& msg);
 int check_hip(fhip_context ctx, hipError_t err, const char* what);
 // Device workspace of at least `bytes`, within the budget (grown only outside capture).
 int acquire_workspace(fhip_context ctx, size_t bytes, void** ptr);
+
+// Looks up this device's copy of the no-alloc scratch array (hipGetSymbolAddress), once per device,
+// with ctx->device current.  Called by fhip_context_create.
+int noalloc_setup(fhip_context ctx);
 
 inline bool valid_scale(float s) { return s > 0.0f && s < __builtin_huge_valf(); }
 

@@ -236,6 +236,12 @@ int fhip_context_create(int device, fhip_context* out) {
         delete ctx;
         return FHIP_ERR_HIP;
     }
+    if (fhip::noalloc_setup(ctx) != FHIP_OK) {
+        (void)hipFree(ctx->scratch);
+        (void)hipStreamDestroy(ctx->own_stream);
+        delete ctx;
+        return FHIP_ERR_HIP;
+    }
     *out = ctx;
     return FHIP_OK;
 }
