@@ -98,12 +98,24 @@ struct HeadParams {
     float* logits;    // optional [m][v]
 };
 
-// Cross-block hand-off without cache-wide fences.  The L2 is per XCD and not coherent between XCDs,
-// so an agent-scope fence writes back and invalidates the whole L2 of the block's XCD -- tens of
-// nanoseconds per block, serialized.  The only data handed over are the per-block keys, so they move
-// with agent-scope atomic stores (written through to the coherent level) and are read back with
-// agent-scope atomic loads; `s_waitcnt vmcnt(0)` makes every key store complete before the block
-// takes its ticket, and the ticket atomics are device-coherent.
+// Cross-block hand-off.  Each block stores its per-row keys as agent-scope atomic stores, then takes a
+// ticket; the block that takes the last ticket reads every block's keys with agent-scope atomic loads
+// and writes the tokens.  Two orderings are compiled:
+//   kRelease = true (the m = 1 kernel): the ticket is a release RMW, the last block of each ticket
+//     group acquires the group (acquire fence) and passes it on with an acq_rel RMW on the top counter,
+//     so the final block has acquired every block's key stores through the counters' release
+//     sequences -- HIP's scoped C++ memory model at agent scope, with no reliance on the hardware.  On
+//     gfx950 each release is `buffer_wbl2 sc1; s_waitcnt vmcnt(0)` before the RMW and each acquire a
+//     `buffer_inv sc1` after it; on the C5 head (256 blocks) it costs nothing measurable
+//     (54.0 us per call either way).
+//   kRelease = false (the MFMA kernel, 2 blocks per CU): the same RMWs relaxed, after
+//     `s_waitcnt vmcnt(0)` -- the completion half of LLVM's agent-scope release sequence for gfx942/gfx950
+//     without the L2 write-back (`buffer_wbl2`).  The write-back exists for non-atomic stores that may
+//     sit dirty in one XCD's L2; the keys are agent-scope atomic stores, which the same memory model
+//     keeps coherent across the agent's L2s, and the wait makes each one complete before its block's
+//     ticket is counted; the final block's agent-scope atomic loads are issued after it has seen the
+//     last ticket.  Here the write-back is not free: the release form measured 80.6 us per C5 M=8 call
+//     against 61.8 us.
 __device__ __forceinline__ void publish_key(unsigned long long* slot, unsigned long long key) {
     __hip_atomic_store(slot, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -111,7 +123,7 @@ __device__ __forceinline__ void publish_key(unsigned long long* slot, unsigned l
 // Called by every block after it published its per-row keys to partials[block * stride + j].  The
 // last block to take a ticket reduces all blocks' keys, writes the tokens and re-arms the tickets,
 // so the kernel is replay-safe with no memset.
-template <int STRIDE>
+template <int STRIDE, bool kRelease>
 __device__ __forceinline__ void ticket_and_finish(const unsigned long long* partials, int64_t m,
                                                   ArgmaxScratch* scratch, int64_t* tokens) {
     const int lane = threadIdx.x & 63;
@@ -123,15 +135,21 @@ __device__ __forceinline__ void ticket_and_finish(const unsigned long long* part
         const unsigned int groups = gridDim.x < (unsigned)kTicketGroups ? gridDim.x : (unsigned)kTicketGroups;
         const unsigned int g = blockIdx.x % groups;
         const unsigned int members = (gridDim.x - g + groups - 1) / groups;
-        __builtin_amdgcn_s_waitcnt(0);  // this block's key stores (threads < 16, same wave) are complete
+        // the barrier above orders every thread's key store before the ticket
         bool top = false;
-        const unsigned int t = __hip_atomic_fetch_add(&scratch->group_done[g][0], 1u, __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
+        unsigned int t;
+        if constexpr (kRelease) {
+            t = __hip_atomic_fetch_add(&scratch->group_done[g][0], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            __builtin_amdgcn_s_waitcnt(0);  // this block's key stores (threads < 16, same wave) are complete
+            t = __hip_atomic_fetch_add(&scratch->group_done[g][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         if (t == members - 1) {
-            // every member has counted: re-arm the group
+            // every member has counted: re-arm the group and count the group in `done`
+            if constexpr (kRelease) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
             __hip_atomic_store(&scratch->group_done[g][0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            top = __hip_atomic_fetch_add(&scratch->done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                  groups - 1;
+            top = __hip_atomic_fetch_add(&scratch->done, 1u, kRelease ? __ATOMIC_ACQ_REL : __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT) == groups - 1;
         }
         last = top;
     }
@@ -297,7 +315,7 @@ __global__ __launch_bounds__(kThreads) void gemv_argmax_kernel(const uint8_t* __
             if (((q & 63) >> kShift) % MT == (int)threadIdx.x) b = red[q] > b ? red[q] : b;
         publish_key(&partials[(int64_t)blockIdx.x * MT + threadIdx.x], b);
     }
-    ticket_and_finish<MT>(partials, m, scratch, tokens);
+    ticket_and_finish<MT, true>(partials, m, scratch, tokens);
 }
 
 // ---- m >= 2: MFMA kernel --------------------------------------------------------------------------
@@ -420,7 +438,7 @@ __global__ __launch_bounds__(kThreads) void gemv_argmax_mfma_kernel(const uint8_
     if (my_c == 0) row_key[my_m] = best;
     __syncthreads();
     if (threadIdx.x < 16) publish_key(&partials[(int64_t)blockIdx.x * 16 + threadIdx.x], row_key[threadIdx.x]);
-    ticket_and_finish<16>(partials, m, scratch, tokens);
+    ticket_and_finish<16, false>(partials, m, scratch, tokens);
 }
 
 // Grid and partial-key workspace of one call.  The grid strides over the vocabulary; measured on the C5
