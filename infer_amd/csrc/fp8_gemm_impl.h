@@ -253,8 +253,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
             uint8_t* dst = st + (is_a ? 0 : S::kA) + (slot * NT + wave * 64) * 16;
             // the uniform term varies with kt, so the per-slot sums are not hoisted into live registers
             const uint32_t u = (uint32_t)(slot * S::kRowsPerPass * (is_a ? k : kp) + (int64_t)kt * BK);
-            // a stage past the last is out of the resource's range (operands are below 2^31 bytes)
-            const uint32_t off = kt < nk ? (is_a ? voff_a : voff_b) + u : 0x80000000u;
+            // a stage past the last is out of the resource's range (operands are below 2^31 bytes), and so
+            // are the B rows of the last pass beyond BN (BNP > BN when BN = 224), which no fragment reads
+            const bool live = kt < nk && (is_a || S::BNP == BN || r0 + slot * S::kRowsPerPass < BN);
+            const uint32_t off = live ? (is_a ? voff_a : voff_b) + u : 0x80000000u;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(is_a ? rsrc_a : rsrc_b, (lds_ptr)dst, 16, off, 0, 0, 0);
         }
     };

@@ -207,11 +207,11 @@ def test_fp8_gemv_m1_activation_encode_exact(ctx, dtype, src, m, staged):
 
 @pytest.mark.parametrize("dtype", FP8)
 @pytest.mark.parametrize("out_dtype", [po.BF16, po.FP32])
-@pytest.mark.parametrize("shape", [(300, 3584, 1024), (4096, 1024, 3584)])
+@pytest.mark.parametrize("shape", [(300, 3584, 1024), (4096, 1024, 3584), (4000, 1024, 3584)])
 def test_fp8_gemm_decoded_outputs(ctx, dtype, out_dtype, shape):
     """BF16 / FP32 outputs (the FP8 code decoded with out_scale, as the exported Gemm -> Cast pair) on a
     down-projection-like shape (K = 3584, 128-deep stages) and the up-projection shape (BF16: 256x224
-    tiles): each output must be exactly a decoded FP8 code and those codes meet the FP8 tolerance."""
+    tiles), whole and with a partial last row tile: each output must be exactly a decoded FP8 code and those codes meet the FP8 tolerance."""
     m, k, n = shape
     a, sa, w_nk, w_src, sw, s_out = _linear_case(SEEDS[3] + 17, dtype, m, k, n, 1)
     wt = ctx.prepare_weight(dev(w_src), dtype, k, n, 1, version=8)
@@ -222,7 +222,8 @@ def test_fp8_gemm_decoded_outputs(ctx, dtype, out_dtype, shape):
     got = host(out, np.uint16) if out_dtype == po.BF16 else host(out)
     codes = po.cast_to_fp8(out_dtype, got, dtype, s_out)
     assert np.array_equal(po.cast_from_fp8(dtype, codes, s_out, out_dtype).view(got.dtype), got)
-    rows = np.sort(rng(9).choice(m, 64, replace=False))
+    # sampled rows plus the last ones (m = 4000: a partial last row tile on the 256x224 path)
+    rows = np.union1d(rng(9).choice(m, 64, replace=False), np.arange(m - 8, m))
     ref = po.fp8_gemm(dtype, a[rows], sa, w_nk, sw, True, s_out)
     fp8_linear_check(dtype, codes[rows], ref, a[rows], sa, w_nk, sw, s_out, f"gemm out {out_dtype}")
     wt.release()
