@@ -83,6 +83,18 @@ const char* fhip_last_error(fhip_context ctx);
 /* Name of the kernel path the last call ran (cf. LastCudaFp8MatmulBackend, runtime.h:100-105). */
 const char* fhip_last_backend(fhip_context ctx);
 
+/* ---- tensor memory (the device replicas a BackendContext keeps for a session's tensors:
+ *      AcquireTensorDevice / SyncTensorToHost / ReleaseTensorDevice of the CUDA runtime,
+ *      src/kernel/cuda/runtime.h:106-145) ------------------------------------------------------
+ * alloc/free/upload/download are refused during capture (FHIP_ERR_STATE).  free waits for the work
+ * queued on the context's stream; upload and download are ordered after it and return once the host
+ * bytes have been read or written; copy (device to device) is stream-ordered and may be captured. */
+int fhip_memory_alloc(fhip_context ctx, size_t bytes, void** out);
+int fhip_memory_free(fhip_context ctx, void* ptr);
+int fhip_memory_upload(fhip_context ctx, void* dst, const void* host, size_t bytes);
+int fhip_memory_download(fhip_context ctx, void* host, const void* src, size_t bytes);
+int fhip_memory_copy(fhip_context ctx, void* dst, const void* src, size_t bytes);
+
 /* ---- prepared weights (Prepare(): x86 PackedFp8Rhs, linear_fp8.h:31-81;
  *      CUDA PackFp8WeightColumnMajor + cache, linear_kernels.cuh:211-221, 528-567) ---------- */
 /* Re-lays an immutable linear weight out for the MFMA/GEMV kernels.  dtype: FP8E4M3, FP8E5M2

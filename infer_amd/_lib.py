@@ -38,6 +38,11 @@ SIGNATURES = {
     "fhip_synchronize": (_INT, [_P]),
     "fhip_last_error": (ctypes.c_char_p, [_P]),
     "fhip_last_backend": (ctypes.c_char_p, [_P]),
+    "fhip_memory_alloc": (_INT, [_P, _SZ, _PP]),
+    "fhip_memory_free": (_INT, [_P, _P]),
+    "fhip_memory_upload": (_INT, [_P, _P, _P, _SZ]),
+    "fhip_memory_download": (_INT, [_P, _P, _P, _SZ]),
+    "fhip_memory_copy": (_INT, [_P, _P, _P, _SZ]),
     "fhip_weight_prepare": (_INT, [_P, _P, _INT, _I64, _I64, _INT, _P, _I64, _P, _I64, _U64, _PP]),
     "fhip_weight_prepare_host": (_INT, [_P, _P, _INT, _I64, _I64, _INT, _P, _I64, _P, _I64, _U64, _PP]),
     "fhip_conv_weight_prepare": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _I32, _P, _I64, _P, _I64, _U64, _PP]),

@@ -305,6 +305,58 @@ int fhip_synchronize(fhip_context ctx) {
     return check_hip(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
 }
 
+int fhip_memory_alloc(fhip_context ctx, size_t bytes, void** out) {
+    if (!ctx || !out) return FHIP_ERR_INVALID;
+    *out = nullptr;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    if (ctx->capturing) return set_error(ctx, FHIP_ERR_STATE, "memory_alloc during capture");
+    if (bytes == 0) return FHIP_OK;
+    DeviceGuard guard(ctx->device);
+    return check_hip(ctx, hipMalloc(out, bytes), "hipMalloc(tensor)");
+}
+
+int fhip_memory_free(fhip_context ctx, void* ptr) {
+    if (!ctx) return FHIP_ERR_INVALID;
+    if (!ptr) return FHIP_OK;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    if (ctx->capturing) return set_error(ctx, FHIP_ERR_STATE, "memory_free during capture");
+    DeviceGuard guard(ctx->device);
+    // work still queued on the context's stream may use the allocation
+    int rc = check_hip(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(before free)");
+    if (rc != FHIP_OK) return rc;
+    return check_hip(ctx, hipFree(ptr), "hipFree(tensor)");
+}
+
+int fhip_memory_upload(fhip_context ctx, void* dst, const void* host, size_t bytes) {
+    if (!ctx || (bytes && (!dst || !host))) return FHIP_ERR_INVALID;
+    if (bytes == 0) return FHIP_OK;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    if (ctx->capturing) return set_error(ctx, FHIP_ERR_STATE, "memory_upload during capture");
+    DeviceGuard guard(ctx->device);
+    // ordered after the work already on the stream; the host bytes are consumed before the call returns
+    int rc = check_hip(ctx, hipMemcpyAsync(dst, host, bytes, hipMemcpyHostToDevice, ctx->stream), "hipMemcpyAsync(H2D)");
+    if (rc != FHIP_OK) return rc;
+    return check_hip(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(upload)");
+}
+
+int fhip_memory_download(fhip_context ctx, void* host, const void* src, size_t bytes) {
+    if (!ctx || (bytes && (!host || !src))) return FHIP_ERR_INVALID;
+    if (bytes == 0) return FHIP_OK;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    if (ctx->capturing) return set_error(ctx, FHIP_ERR_STATE, "memory_download during capture");
+    DeviceGuard guard(ctx->device);
+    int rc = check_hip(ctx, hipMemcpyAsync(host, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpyAsync(D2H)");
+    if (rc != FHIP_OK) return rc;
+    return check_hip(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(download)");
+}
+
+int fhip_memory_copy(fhip_context ctx, void* dst, const void* src, size_t bytes) {
+    if (!ctx || (bytes && (!dst || !src))) return FHIP_ERR_INVALID;
+    if (bytes == 0) return FHIP_OK;
+    DeviceGuard guard(ctx->device);
+    return check_hip(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream), "hipMemcpyAsync(D2D)");
+}
+
 const char* fhip_last_error(fhip_context ctx) { return ctx ? ctx->last_error.c_str() : "null context"; }
 const char* fhip_last_backend(fhip_context ctx) { return ctx ? ctx->last_backend : ""; }
 
