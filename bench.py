@@ -269,9 +269,10 @@ def _time_calls(fn, seconds, min_calls=5):
 
 def cpu_configs(args):
     """CPU baselines of the other configs on the host cores, each a bounded sample (~3 s).
-    C3 and C5 run the reference's own x86 kernels (oracle/_ref, its thread policy: min(4, OpenMP) workers);
-    C1 and C4 run the C restatement of the reference's Common kernels (oracle/liboracle.so: the x86 INT8
-    FC is single-threaded in the reference, its conv uses every OpenMP thread)."""
+    With oracle/_ref present every config runs the reference's own x86 kernels, with its thread policy:
+    INT8 Gemm 1 thread (x86/int8.cc:514-572), INT8 conv every OpenMP thread (int8.cc:2331-2334), FP8 linear
+    and BF16 argmax min(4, OpenMP) workers.  Without it, C1 and C4 fall back to the C restatement of the
+    Common kernels (oracle/liboracle.so, "kind": "port")."""
     import numpy as np
     from oracle import pyoracle as po
     res = {}
@@ -279,28 +280,53 @@ def cpu_configs(args):
     r = np.random.default_rng(0xFEA70010)
     L = po.lib()
     all_threads = L.fo_set_threads(0)
+    have_ref = po.ref_available()
     # C1: QuantizeLinear -> INT8 Gemm (transB) -> DequantizeLinear is dominated by the Gemm; 1 thread
     m, k, n = 128, 1024, 1024
     a = r.integers(-127, 128, (m, k)).astype(np.int8)
     w = r.integers(-127, 128, (n, k)).astype(np.int8)
     ws = r.uniform(1e-3, 1e-2, n).astype(np.float32)
     bias = r.integers(-20000, 20000, n).astype(np.int32)
-    L.fo_set_threads(1)
-    med, calls = _time_calls(lambda: po.i8_linear(po.I8_GEMM, a, 0.03, 0, w, True, ws, None, bias, po.BIAS_VECTOR, 1.0,
-                                                  1.0, 0.05, 0), budget)
-    res["C1"] = {"value": 2.0 * m * k * n / med / 1e12, "unit": "TOPS", "cores": 1, "kind": "port",
-                 "sample": f"{calls} calls of the INT8 Gemm 128x1024x1024 restated from the Common kernel, "
-                           f"median {med * 1e3:.2f} ms"}
+    if have_ref:
+        R = po.ref()
+        R.ref_set_threads(1)
+        h = R.ref_i8_gemm_create(po._ptr(a), 0.03, 0, m, k, po._ptr(w), po._ptr(ws), n, n, po._ptr(bias), 1.0, 1.0,
+                                 0.05, 0)
+        med, calls = _time_calls(lambda: R.ref_i8_gemm_compute(h), budget)
+        R.ref_i8_gemm_destroy(h)
+        res["C1"] = {"value": 2.0 * m * k * n / med / 1e12, "unit": "TOPS", "cores": 1, "kind": "reference",
+                     "sample": f"{calls} calls of Feather x86 GemmKernel<X86, INT8> (int8.cc:514-572), "
+                               f"128x1024x1024 transB, median {med * 1e3:.1f} ms; the Common QuantizeLinear and "
+                               f"DequantizeLinear nodes are not included"}
+    else:
+        L.fo_set_threads(1)
+        med, calls = _time_calls(lambda: po.i8_linear(po.I8_GEMM, a, 0.03, 0, w, True, ws, None, bias, po.BIAS_VECTOR,
+                                                      1.0, 1.0, 0.05, 0), budget)
+        res["C1"] = {"value": 2.0 * m * k * n / med / 1e12, "unit": "TOPS", "cores": 1, "kind": "port",
+                     "sample": f"{calls} calls of the INT8 Gemm 128x1024x1024 restated from the Common kernel, "
+                               f"median {med * 1e3:.2f} ms"}
     # C4: INT8 conv 3x3 s2 p1, all threads
     L.fo_set_threads(all_threads)
     x = r.integers(-128, 128, (1, 64, 160, 160)).astype(np.int8)
     wc = r.integers(-127, 128, (128, 64, 3, 3)).astype(np.int8)
     wcs = r.uniform(1e-3, 1e-2, 128).astype(np.float32)
     cb = r.integers(-5000, 5000, 128).astype(np.int32)
-    med, calls = _time_calls(lambda: po.i8_conv2d(x, 0.05, 0, wc, wcs, cb, 2, 1, 0.5, 0), budget)
-    res["C4"] = {"value": 943718400 / med / 1e12, "unit": "TOPS", "cores": all_threads, "kind": "port",
-                 "sample": f"{calls} calls of the INT8 Conv2D [1,64,160,160] x [128,64,3,3] s2 p1 restated from the "
-                           f"Common kernel, median {med * 1e3:.1f} ms"}
+    if have_ref:
+        R.ref_set_threads(all_threads)
+        h = R.ref_i8_conv2d_create(po._ptr(x), 1, 64, 160, 160, 0.05, 0, po._ptr(wc), 128, 3, 3, po._ptr(wcs),
+                                   po._ptr(cb), 2, 1, 80, 80, 0.5, 0)
+        R.ref_i8_conv2d_compute(h)  # packs the weights once, as Prepare-time caching does
+        med, calls = _time_calls(lambda: R.ref_i8_conv2d_compute(h), budget)
+        R.ref_i8_conv2d_destroy(h)
+        path = "VNNI" if R.ref_has_avx_vnni() else "AVX2 maddubs"
+        res["C4"] = {"value": 943718400 / med / 1e12, "unit": "TOPS", "cores": all_threads, "kind": "reference",
+                     "sample": f"{calls} calls of Feather x86 Conv2DKernel<X86, INT8> ({path} path, int8.cc:684-2346), "
+                               f"[1,64,160,160] x [128,64,3,3] s2 p1, median {med * 1e3:.2f} ms"}
+    else:
+        med, calls = _time_calls(lambda: po.i8_conv2d(x, 0.05, 0, wc, wcs, cb, 2, 1, 0.5, 0), budget)
+        res["C4"] = {"value": 943718400 / med / 1e12, "unit": "TOPS", "cores": all_threads, "kind": "port",
+                     "sample": f"{calls} calls of the INT8 Conv2D [1,64,160,160] x [128,64,3,3] s2 p1 restated from "
+                               f"the Common kernel, median {med * 1e3:.1f} ms"}
     if po.ref_available():
         R = po.ref()
         threads = min(4, R.ref_max_threads())

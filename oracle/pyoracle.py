@@ -104,6 +104,17 @@ def ref():
         _sig(R, "ref_bf16_argmax_create", _P, _P, _I64, _I64)
         _sig(R, "ref_bf16_argmax_compute", _INT, _P, _P, ctypes.POINTER(ctypes.c_int64))
         _sig(R, "ref_bf16_argmax_destroy", None, _P)
+        _sig(R, "ref_i8_gemm_create", _P, _P, _F, _I32, _I64, _I64, _P, _P, _I64, _I64, _P, _F, _F, _F, _I32)
+        _sig(R, "ref_i8_gemm_compute", _INT, _P)
+        _sig(R, "ref_i8_gemm_output", None, _P, _P)
+        _sig(R, "ref_i8_gemm_destroy", None, _P)
+        _sig(R, "ref_i8_conv2d_create", _P, _P, _I64, _I64, _I64, _I64, _F, _I32, _P, _I64, _I64, _I64, _P, _P,
+             _I32, _I32, _I64, _I64, _F, _I32)
+        _sig(R, "ref_i8_conv2d_compute", _INT, _P)
+        _sig(R, "ref_i8_conv2d_output", None, _P, _P)
+        _sig(R, "ref_i8_conv2d_destroy", None, _P)
+        _sig(R, "ref_has_avx_vnni", _INT)
+        _sig(R, "ref_set_threads", None, _INT)
         _ref = R
     return _ref
 
