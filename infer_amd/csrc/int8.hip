@@ -17,6 +17,7 @@
 #include "fhip_internal.h"
 #include "codec.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace {
@@ -32,6 +33,18 @@ __device__ __forceinline__ int8_t clamp_round_i8(double t) {
     return (int8_t)lo;
 }
 
+// clamp_round_i8(real / s_out + zp_out), the reference's requantization (int8_kernel_utils.h:155-179),
+// without a double division on the common path.  t = real * (1 / s_out) + zp_out differs from the divided
+// form by at most ~2^-51 * (|t| + |zp_out|) (the reciprocal and the product are each correctly rounded);
+// round() changes value only at the x.5 points, so wherever t is farther than that from one both forms
+// round to the same integer.  Only near an x.5 point (or for non-finite t) is the division done.
+__device__ __forceinline__ int8_t requant_i8(double real, double s_out, double recip_out, double zp_out) {
+    const double t = real * recip_out + zp_out;
+    const double half_gap = fabs((t - floor(t)) - 0.5);
+    if (!(half_gap > 0x1p-40 * (fabs(t) + 256.0))) return clamp_round_i8(real / s_out + zp_out);
+    return clamp_round_i8(t);
+}
+
 struct I8Epilogue {
     int kind;
     const float* w_scales;   // [n] (per-tensor weights: all equal)
@@ -43,6 +56,7 @@ struct I8Epilogue {
     double alpha, beta;
     double inv_out_den;      // double(s_out), used as a divisor
     double zp_out;
+    double recip_out;        // 1 / double(s_out), for requant_i8
     int8_t* out;
     int64_t ldo;
     // Fused DequantizeLinear (per tensor): out_dtype FP32/FP16/BF16 writes float((q - dq_zp) * dq_scale) with
@@ -77,7 +91,7 @@ struct I8Epilogue {
         } else {
             real = (double)(dot + b) * scale;  // MatMul has no bias (b = 0)
         }
-        const int8_t q = clamp_round_i8(real / inv_out_den + zp_out);
+        const int8_t q = requant_i8(real, inv_out_den, recip_out, zp_out);
         const int64_t idx = row * ldo + col;
         if (out_dtype == FHIP_INT8) {
             out[idx] = q;
@@ -290,7 +304,7 @@ __global__ __launch_bounds__(256) void i8_conv_kernel(const int8_t* __restrict__
                 const double real = (double)total * ((double)ep.s_a * (double)ep.w_scales[oc]);
                 const int64_t off = g.layout == FHIP_NCHW ? ((b * (g.ocg * gridDim.z) + oc) * g.oh + oy) * g.ow + ox
                                                           : ((b * g.oh + oy) * g.ow + ox) * (g.ocg * gridDim.z) + oc;
-                ep.out[off] = clamp_round_i8(real / ep.inv_out_den + ep.zp_out);
+                ep.out[off] = requant_i8(real, ep.inv_out_den, ep.recip_out, ep.zp_out);
             }
         }
 }
@@ -309,6 +323,11 @@ constexpr int kConvPitch = 80;  // 64 channels + 16 bytes: stride-2 fragment rea
 // channel (the columns plus up to 3 bytes of alignment shift); windows up to 4 * kWinCols = 80 columns.
 constexpr int kWinCols = 20;
 constexpr int kWinSpan = kWinCols / 4 + 1;
+// NCHW 16-byte staging: the window is widened to whole aligned 16-byte chunks of each input row (at most
+// kWinChunks), so a thread loads 4 channels x one chunk with four 16-byte loads; rows a multiple of 16 bytes
+// make every chunk either wholly inside the row or wholly padding.
+constexpr int kWinChunks = 5;
+__host__ __device__ constexpr int conv_chunks(int wx) { return (wx + 15 + 15) / 16; }
 
 template <int WNF, int TAPS>
 __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __restrict__ in, ConvGeom g,
@@ -353,8 +372,16 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
     }
     const int ix0 = (int)(ox0 * g.sw - g.pw);
     const uint8_t zp = (uint8_t)g.zp_in;
-    // NCHW fast path: rows 4-byte aligned, at most 4 tap rows, a window of at most 80 columns.
-    const bool dword_rows = g.layout == FHIP_NCHW && (g.w & 3) == 0 &&
+    // NCHW 16-byte path: rows a multiple of 16 bytes, 16-byte aligned input, kh * 16 * chunks threads.
+    const int chunks = conv_chunks(wx);
+    const bool vec_rows = g.layout == FHIP_NCHW && (g.w & 15) == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0 &&
+                          chunks <= kWinChunks && g.kh * 16 * chunks <= 256;
+    // window row length in LDS and the column of the first window byte in it
+    const int wrow = vec_rows ? 16 * chunks : wx;
+    const int a0 = ix0 >= 0 ? ix0 & ~15 : -((-ix0 + 15) & ~15);  // floor to a multiple of 16
+    const int xsh = vec_rows ? ix0 - a0 : 0;
+    // NCHW dword path: rows 4-byte aligned, at most 4 tap rows, a window of at most 80 columns.
+    const bool dword_rows = !vec_rows && g.layout == FHIP_NCHW && (g.w & 3) == 0 &&
                             (reinterpret_cast<uintptr_t>(in) & 3) == 0 && wx <= 4 * kWinCols && g.kh * 64 <= 256;
     for (int64_t c0 = 0; c0 < g.c; c0 += 64) {
         // 1. issue this thread's window loads (fast path), then every tap's weight fragments; nothing
@@ -362,7 +389,22 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
         // thread t: tap row ky = t / 64, channels 4*cq .. 4*cq+3 with cq = (t / 4) % 16, window columns
         // [20*xq, 20*xq + 20) with xq = t % 4; per channel the columns come as kWinSpan aligned dwords
         uint32_t d[4][kWinSpan];
+        uint4 q16[4];
         int sh = 0;
+        // 16-byte path: thread t = (ky * 16 + cq) * chunks + xq loads chunk xq (columns a0 + 16 xq ..) of
+        // channels 4 cq .. 4 cq + 3 of tap row ky; consecutive lanes read consecutive chunks of a row
+        if (vec_rows && tid < g.kh * 16 * chunks) {
+            const int xq = tid % chunks, cq = (tid / chunks) & 15, ky = tid / (16 * chunks);
+            const int iy = (int)(oy * g.sh - g.ph) + ky * (int)g.dh;
+            const int gx = a0 + 16 * xq;
+            const bool live = iy >= 0 && iy < (int)g.h && gx >= 0 && gx < (int)g.w;
+            const uint32_t z = (uint32_t)zp * 0x01010101u;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int8_t* src = in + ((b * g.c + c0 + 4 * cq + c) * g.h + (live ? iy : 0)) * g.w + (live ? gx : 0);
+                q16[c] = live ? *reinterpret_cast<const uint4*>(src) : make_uint4(z, z, z, z);
+            }
+        }
         if (dword_rows) {
             const int ky = tid >> 6, cq = (tid >> 2) & 15, xq = tid & 3;
             const int iy = (int)(oy * g.sh - g.ph) + ky * (int)g.dh;
@@ -396,7 +438,30 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
             __builtin_amdgcn_s_barrier();
         }
         // 3. stage the window (channel-last in LDS)
-        if (dword_rows) {
+        if (vec_rows) {
+            if (tid < g.kh * 16 * chunks) {
+                const int xq = tid % chunks, cq = (tid / chunks) & 15, ky = tid / (16 * chunks);
+                uint8_t* dst = win + (ky * wrow + 16 * xq) * kConvPitch + 4 * cq;
+                const uint32_t w4[4][4] = {{q16[0].x, q16[0].y, q16[0].z, q16[0].w},
+                                           {q16[1].x, q16[1].y, q16[1].z, q16[1].w},
+                                           {q16[2].x, q16[2].y, q16[2].z, q16[2].w},
+                                           {q16[3].x, q16[3].y, q16[3].z, q16[3].w}};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    // w4[c][i] holds columns 4i .. 4i+3 of channel c: transpose to one dword (4 channels) per column
+                    const uint32_t lo01 = __builtin_amdgcn_perm(w4[1][i], w4[0][i], 0x05010400u);
+                    const uint32_t hi01 = __builtin_amdgcn_perm(w4[1][i], w4[0][i], 0x07030602u);
+                    const uint32_t lo23 = __builtin_amdgcn_perm(w4[3][i], w4[2][i], 0x05010400u);
+                    const uint32_t hi23 = __builtin_amdgcn_perm(w4[3][i], w4[2][i], 0x07030602u);
+                    const uint32_t col[4] = {__builtin_amdgcn_perm(lo23, lo01, 0x05040100u),
+                                             __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
+                                             __builtin_amdgcn_perm(hi23, hi01, 0x05040100u),
+                                             __builtin_amdgcn_perm(hi23, hi01, 0x07060302u)};
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) *reinterpret_cast<uint32_t*>(dst + (4 * i + u) * kConvPitch) = col[u];
+                }
+            }
+        } else if (dword_rows) {
             if (tid < g.kh * 64) {
                 const int ky = tid >> 6, cq = (tid >> 2) & 15, x0 = (tid & 3) * kWinCols;
                 uint8_t* dst = win + (ky * wx + x0) * kConvPitch + 4 * cq;
@@ -486,7 +551,7 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
             for (int f = 0; f < 2; ++f) {
                 const int p = f * 16 + (lane & 15);
                 const int x = p * g.sw + (int)(kx * g.dw);
-                const uint4 v = *reinterpret_cast<const uint4*>(win + (ky * wx + x) * kConvPitch + kq);
+                const uint4 v = *reinterpret_cast<const uint4*>(win + (ky * wrow + x + xsh) * kConvPitch + kq);
                 af[f] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
             }
 #pragma unroll
@@ -520,7 +585,7 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const double real = (double)(acc[f][j][r] + shift) * scale;
-                q[r] = clamp_round_i8(real / ep.inv_out_den + ep.zp_out);
+                q[r] = requant_i8(real, ep.inv_out_den, ep.recip_out, ep.zp_out);
             }
             const uint32_t packed = (uint32_t)(uint8_t)q[0] | ((uint32_t)(uint8_t)q[1] << 8) |
                                     ((uint32_t)(uint8_t)q[2] << 16) | ((uint32_t)(uint8_t)q[3] << 24);
@@ -669,7 +734,7 @@ int fhip_i8_linear_ex(fhip_context ctx, int kind, const int8_t* a, float s_a, in
                               (double)s_a * (double)w->max_scale / (double)s_out;
     if (!(real_bound < 1e300)) return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "i8_linear: scales too large");
     I8Epilogue ep{kind, w->scales, w->wsum, bias, bias_kind, zp_a, s_a, (double)alpha, (double)beta, (double)s_out,
-                  (double)zp_out, static_cast<int8_t*>(out), w->n};
+                  (double)zp_out, 1.0 / (double)s_out, static_cast<int8_t*>(out), w->n};
     ep.out_dtype = out_dtype;
     ep.dq_scale = dq_scale;
     ep.dq_zp = dq_zp;
@@ -716,11 +781,12 @@ int fhip_i8_conv2d(fhip_context ctx, const int8_t* in, int64_t n, int64_t c, int
     ConvGeom g{n, c, h, w, oh, ow, wt->icg, wt->kh, wt->kw, wt->n / wt->group, wt->k, ((wt->k + 127) / 128) * 128,
                stride_h, stride_w, pad_h, pad_w, dil_h, dil_w, layout, (int8_t)zp_in};
     I8Epilogue ep{FHIP_I8_FC, wt->scales, wt->wsum, nullptr, FHIP_BIAS_NONE, zp_in, s_in, 1.0, 1.0, (double)s_out,
-                  (double)zp_out, out, 0};
+                  (double)zp_out, 1.0 / (double)s_out, out, 0};
     if (wt->tap_major && c % 64 == 0 && wt->group == 1 &&
         (layout == FHIP_NCHW || (reinterpret_cast<uintptr_t>(in) & 15) == 0)) {
         const int wx = (kConvTox - 1) * stride_w + (int)((wt->kw - 1) * dil_w) + 1;
-        const size_t lds = (size_t)wt->kh * wx * kConvPitch;
+        // room for the 16-byte path's widened window (the kernel picks the path; either fits)
+        const size_t lds = (size_t)wt->kh * std::max(wx, 16 * conv_chunks(wx)) * kConvPitch;
         if (lds <= 64 * 1024) {
             const int64_t oc = wt->n;
             const int wnf = oc >= 128 ? 2 : 1;
