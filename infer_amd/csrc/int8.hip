@@ -318,6 +318,7 @@ __global__ __launch_bounds__(256) void i8_conv_kernel(const int8_t* __restrict__
 // (chunk, ky, kx, 64 channels) with v_mfma_i32_16x16x64_i8; integer accumulation is exact, so the
 // order differs from the reference's (ci, ky, kx) order without changing any sum.
 constexpr int kConvTox = 32;
+constexpr int kConvFrags = kConvTox / 16;  // 16-pixel A fragments per block
 constexpr int kConvPitch = 80;  // 64 channels + 16 bytes: stride-2 fragment reads spread over banks
 // NCHW fast staging: a thread covers kWinCols window columns of 4 channels, kWinSpan aligned dwords per
 // channel (the columns plus up to 3 bytes of alignment shift); windows up to 4 * kWinCols = 80 columns.
@@ -344,9 +345,9 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
     const int wx = (kConvTox - 1) * g.sw + (int)((g.kw - 1) * g.dw) + 1;
     const int64_t taps = g.kh * g.kw;
     const int kq = (lane >> 4) * 16;  // channel quarter of this lane's fragment
-    v4i acc[2][WNF];
+    v4i acc[kConvFrags][WNF];
 #pragma unroll
-    for (int f = 0; f < 2; ++f)
+    for (int f = 0; f < kConvFrags; ++f)
 #pragma unroll
         for (int j = 0; j < WNF; ++j) acc[f][j] = v4i{0, 0, 0, 0};
 
@@ -546,16 +547,16 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
         }
         __syncthreads();
         auto tap_step = [&](int64_t ky, int64_t kx, const v4i (&bf)[WNF]) {
-            v4i af[2];
+            v4i af[kConvFrags];
 #pragma unroll
-            for (int f = 0; f < 2; ++f) {
+            for (int f = 0; f < kConvFrags; ++f) {
                 const int p = f * 16 + (lane & 15);
                 const int x = p * g.sw + (int)(kx * g.dw);
                 const uint4 v = *reinterpret_cast<const uint4*>(win + (ky * wrow + x + xsh) * kConvPitch + kq);
                 af[f] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
             }
 #pragma unroll
-            for (int f = 0; f < 2; ++f)
+            for (int f = 0; f < kConvFrags; ++f)
 #pragma unroll
                 for (int j = 0; j < WNF; ++j)
                     acc[f][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[f], bf[j], acc[f][j], 0, 0, 0);
@@ -574,7 +575,7 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
     }
     // C fragment of lane l: channel l%16, pixels 4*(l/16) .. +3 (consecutive output x).
 #pragma unroll
-    for (int f = 0; f < 2; ++f)
+    for (int f = 0; f < kConvFrags; ++f)
 #pragma unroll
         for (int j = 0; j < WNF; ++j) {
             const int64_t oc = oc_base + j * 16 + (lane & 15);
