@@ -155,9 +155,15 @@ int HipExecutionContext::AcquireLinearWeight(const Tensor& w, int dtype, int64_t
         *out = hit->second;
         return FHIP_OK;
     }
+    // An immutable weight (a WeightStore view of the mmapped model file, src/model/weight_store.cc:77-104) is
+    // prepared straight from its host bytes: no raw device replica is kept beside the prepared copy.
+    const bool from_host = w.is_immutable();
     const void* device = nullptr;
-    int rc = AcquireInput(w, &device);
-    if (rc != FHIP_OK) return rc;
+    int rc = FHIP_OK;
+    if (!from_host) {
+        rc = AcquireInput(w, &device);
+        if (rc != FHIP_OK) return rc;
+    }
     const auto& q = w.quantization();
     std::vector<float> scales;
     std::vector<int32_t> zero_points;
@@ -167,9 +173,12 @@ int HipExecutionContext::AcquireLinearWeight(const Tensor& w, int dtype, int64_t
         zero_points = q.zero_points.empty() ? std::vector<int32_t>{q.zero_point_at(0)} : q.zero_points;
     }
     fhip_weight handle = nullptr;
-    rc = fhip_weight_prepare(ctx_, device, dtype, k, n, layout, scales.empty() ? nullptr : scales.data(),
-                             static_cast<int64_t>(scales.size()), zero_points.empty() ? nullptr : zero_points.data(),
-                             static_cast<int64_t>(zero_points.size()), w.mutation_version(), &handle);
+    const float* sp = scales.empty() ? nullptr : scales.data();
+    const int32_t* zp = zero_points.empty() ? nullptr : zero_points.data();
+    rc = from_host ? fhip_weight_prepare_host(ctx_, w.raw_data(), dtype, k, n, layout, sp, static_cast<int64_t>(scales.size()),
+                                              zp, static_cast<int64_t>(zero_points.size()), w.mutation_version(), &handle)
+                   : fhip_weight_prepare(ctx_, device, dtype, k, n, layout, sp, static_cast<int64_t>(scales.size()), zp,
+                                         static_cast<int64_t>(zero_points.size()), w.mutation_version(), &handle);
     if (rc != FHIP_OK) return rc;
     weights_[key] = handle;
     *out = handle;
