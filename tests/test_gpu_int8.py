@@ -219,12 +219,14 @@ def test_i8_conv_groups_dilation_zero_point(ctx, layout):
 
 
 @pytest.mark.parametrize("layout", [0, 1])
-@pytest.mark.parametrize("wd,pad", [(23, (1, 0)), (76, (1, 1))])
+@pytest.mark.parametrize("wd,pad", [(23, (1, 0)), (76, (1, 1)), (96, (1, 1)), (160, (0, 3))])
 def test_i8_conv_window_path_general_geometry(ctx, layout, wd, pad):
     """The LDS-window conv kernel (group 1, IC % 64 == 0) on a ragged shape: OC not a multiple of 64,
     asymmetric stride/pad/dilation, non-zero input zero point, output width not a multiple of 32.
     Width 23 stages NCHW rows byte by byte; width 76 (rows 4-byte aligned, odd left pad, two blocks per
-    output row) takes the aligned-dword staging with a 3-byte shift."""
+    output row) takes the aligned-dword staging with a 3-byte shift; widths 96 and 160 (rows a multiple of
+    16 bytes) take the 16-byte chunk staging, with left pads 1 and 3 (window starts before the row, chunk
+    offsets 15 and 13) and chunks past the right edge."""
     r = rng(41)
     n, c, h, oc = 2, 128, 17, 80
     x = r.integers(-128, 128, (n, c, h, wd)).astype(np.int8)
