@@ -145,6 +145,22 @@ int HipExecutionContext::CopyReplica(Tensor& dst, const Tensor& src, size_t byte
     return fhip_memory_copy(ctx_, to, from, bytes);
 }
 
+// A mutated weight gets a new prepared copy under its new version; the copies of its older versions are
+// released so a weight updated in place does not accumulate prepared copies.
+void HipExecutionContext::ReleaseStaleWeights(const WeightKey& fresh) {
+    for (auto it = weights_.begin(); it != weights_.end();) {
+        const auto& k = it->first;
+        if (std::get<0>(k) == std::get<0>(fresh) && std::get<1>(k) == std::get<1>(fresh) &&
+            std::get<3>(k) == std::get<3>(fresh) && std::get<4>(k) == std::get<4>(fresh) &&
+            std::get<2>(k) != std::get<2>(fresh)) {
+            (void)fhip_weight_release(it->second);
+            it = weights_.erase(it);
+        } else {
+            ++it;
+        }
+    }
+}
+
 int HipExecutionContext::AcquireLinearWeight(const Tensor& w, int dtype, int64_t k, int64_t n, int layout,
                                              fhip_weight* out) {
     std::lock_guard<std::recursive_mutex> lock(mu_);
@@ -180,6 +196,7 @@ int HipExecutionContext::AcquireLinearWeight(const Tensor& w, int dtype, int64_t
                    : fhip_weight_prepare(ctx_, device, dtype, k, n, layout, sp, static_cast<int64_t>(scales.size()), zp,
                                          static_cast<int64_t>(zero_points.size()), w.mutation_version(), &handle);
     if (rc != FHIP_OK) return rc;
+    ReleaseStaleWeights(key);
     weights_[key] = handle;
     *out = handle;
     return FHIP_OK;
@@ -208,6 +225,7 @@ int HipExecutionContext::AcquireConvWeight(const Tensor& w, int32_t group, fhip_
                                   scales.data(), static_cast<int64_t>(scales.size()), zero_points.data(),
                                   static_cast<int64_t>(zero_points.size()), w.mutation_version(), &handle);
     if (rc != FHIP_OK) return rc;
+    ReleaseStaleWeights(key);
     weights_[key] = handle;
     *out = handle;
     return FHIP_OK;

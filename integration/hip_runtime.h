@@ -71,6 +71,7 @@ class HipExecutionContext {
     };
     using WeightKey = std::tuple<uint64_t, size_t, uint64_t, int, int, int64_t>;
     static Key KeyOf(const Tensor& tensor, size_t bytes);
+    void ReleaseStaleWeights(const WeightKey& fresh);
     Replica* Find(const Tensor& tensor);
     int Ensure(const Tensor& tensor, size_t bytes, Replica** out);
 
