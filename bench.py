@@ -313,8 +313,8 @@ def cpu_configs(args):
     cb = r.integers(-5000, 5000, 128).astype(np.int32)
     if have_ref:
         R.ref_set_threads(all_threads)
-        h = R.ref_i8_conv2d_create(po._ptr(x), 1, 64, 160, 160, 0.05, 0, po._ptr(wc), 128, 3, 3, po._ptr(wcs),
-                                   po._ptr(cb), 2, 1, 80, 80, 0.5, 0)
+        h = R.ref_i8_conv2d_create(po._ptr(x), 1, 64, 160, 160, 0, 0.05, 0, po._ptr(wc), 128, 3, 3, 1, po._ptr(wcs),
+                                   po._ptr(cb), 2, 2, 1, 1, 1, 1, 80, 80, 0.5, 0)
         R.ref_i8_conv2d_compute(h)  # packs the weights once, as Prepare-time caching does
         med, calls = _time_calls(lambda: R.ref_i8_conv2d_compute(h), budget)
         R.ref_i8_conv2d_destroy(h)

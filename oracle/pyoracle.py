@@ -108,8 +108,8 @@ def ref():
         _sig(R, "ref_i8_gemm_compute", _INT, _P)
         _sig(R, "ref_i8_gemm_output", None, _P, _P)
         _sig(R, "ref_i8_gemm_destroy", None, _P)
-        _sig(R, "ref_i8_conv2d_create", _P, _P, _I64, _I64, _I64, _I64, _F, _I32, _P, _I64, _I64, _I64, _P, _P,
-             _I32, _I32, _I64, _I64, _F, _I32)
+        _sig(R, "ref_i8_conv2d_create", _P, _P, _I64, _I64, _I64, _I64, _INT, _F, _I32, _P, _I64, _I64, _I64, _I32,
+             _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I64, _I64, _F, _I32)
         _sig(R, "ref_i8_conv2d_compute", _INT, _P)
         _sig(R, "ref_i8_conv2d_output", None, _P, _P)
         _sig(R, "ref_i8_conv2d_destroy", None, _P)

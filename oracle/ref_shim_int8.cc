@@ -118,25 +118,36 @@ void ref_i8_gemm_output(void* opaque, int8_t* out) {
 
 void ref_i8_gemm_destroy(void* opaque) { delete static_cast<I8Gemm*>(opaque); }
 
-// Conv2D, INT8 NCHW, group 1, per-tensor activation/output, per-output-channel weight scales,
-// INT32 bias [OC] or none.
-void* ref_i8_conv2d_create(const int8_t* x, int64_t n, int64_t c, int64_t h, int64_t w, float s_in, int32_t zp_in,
-                           const int8_t* wt, int64_t oc, int64_t kh, int64_t kw, const float* s_w, const int32_t* bias,
-                           int32_t stride, int32_t pad, int64_t oh, int64_t ow, float s_out, int32_t zp_out) {
+// Conv2D, INT8, NCHW (layout 0) or NHWC (layout 1) activations, weight [OC, C/group, KH, KW],
+// per-tensor activation/output, per-output-channel weight scales, INT32 bias [OC] or none.
+void* ref_i8_conv2d_create(const int8_t* x, int64_t n, int64_t c, int64_t h, int64_t w, int layout, float s_in,
+                           int32_t zp_in, const int8_t* wt, int64_t oc, int64_t kh, int64_t kw, int32_t group,
+                           const float* s_w, const int32_t* bias, int32_t stride_h, int32_t stride_w, int32_t pad_h,
+                           int32_t pad_w, int32_t dil_h, int32_t dil_w, int64_t oh, int64_t ow, float s_out,
+                           int32_t zp_out) {
     auto* hd = new I8Conv();
     hd->param = std::make_shared<feather::operators::Conv2dParam>();
     auto& p = *hd->param;
-    p.input = MakeTensor<int8_t>(x, {n, c, h, w}, DataType::INT8);
-    p.input->set_layout(DataLayout::NCHW);
+    const DataLayout lay = layout == 1 ? DataLayout::NHWC : DataLayout::NCHW;
+    const std::vector<int64_t> in_shape = layout == 1 ? std::vector<int64_t>{n, h, w, c} : std::vector<int64_t>{n, c, h, w};
+    const std::vector<int64_t> out_shape =
+        layout == 1 ? std::vector<int64_t>{n, oh, ow, oc} : std::vector<int64_t>{n, oc, oh, ow};
+    p.input = MakeTensor<int8_t>(x, in_shape, DataType::INT8);
+    p.input->set_layout(lay);
     p.input->set_quantization(PerTensor(s_in, zp_in));
-    p.w = MakeTensor<int8_t>(wt, {oc, c, kh, kw}, DataType::INT8);
+    p.w = MakeTensor<int8_t>(wt, {oc, c / group, kh, kw}, DataType::INT8);
     p.w->set_quantization(PerChannel(s_w, oc, 0));
     if (bias) p.bias = MakeTensor<int32_t>(bias, {oc}, DataType::INT32);
-    p.out = MakeTensor<int8_t>(nullptr, {n, oc, oh, ow}, DataType::INT8);
-    p.out->set_layout(DataLayout::NCHW);
+    p.out = MakeTensor<int8_t>(nullptr, out_shape, DataType::INT8);
+    p.out->set_layout(lay);
     p.out->set_quantization(PerTensor(s_out, zp_out));
-    p.stride_h = p.stride_w = stride;
-    p.pad_h = p.pad_w = pad;
+    p.stride_h = stride_h;
+    p.stride_w = stride_w;
+    p.pad_h = pad_h;
+    p.pad_w = pad_w;
+    p.dilation_h = dil_h;
+    p.dilation_w = dil_w;
+    p.group = group;
     hd->kernel.SetParamOwner(hd->param);
     return hd;
 }
