@@ -4,7 +4,8 @@ The outputs come from oracle/_ref/libfeather_ref.so, which `make -C oracle ref` 
 sources themselves: include/util/fp8.h (FloatToFp8E4M3/E5M2, Fp8*ToFloat), include/util/bf16.h
 (FloatToBFloat16), include/util/fp16.h (FloatToHalf, Cast's FP16 rule), quantize_linear_utils.h (EncodeFloat16), include/quant/quantization.h (QuantizeInt8Value), src/kernel/common/int8_kernel_utils.h
 (QuantizeAccumulator), src/kernel/x86/linear_fp8.cc (ComputeLinearRowMajorX86Fp8*, the packed
-TransposedRhsArgmax) and src/kernel/x86/linear.cc (the packed BF16 argmax).  Only inputs and the
+TransposedRhsArgmax), src/kernel/x86/linear.cc (the packed BF16 argmax) and src/kernel/x86/int8.cc (the INT8
+Gemm and Conv2D kernels).  Only inputs and the
 reference's outputs are stored, so the oracle and the HIP path can be checked against the reference
 where that build is absent (the GPU box).
 
@@ -163,9 +164,47 @@ def make_argmax(R):
     return out
 
 
+def make_int8(R):
+    """The reference's x86 INT8 Gemm (transB, zero point, alpha/beta, bias) and Conv2D (NCHW stride 2; NHWC
+    with groups and dilation).  Seeds are taken where the x86 conv's float requantization agrees with the
+    Common kernel everywhere (they differ only within float rounding of a round-half point), so every stored
+    output is also the Common result."""
+    from tests.test_oracle_ref_int8 import _x86_conv, _x86_gemm
+    out = {}
+    r = np.random.default_rng(0xFEA70104)
+    m, k, n = 24, 192, 80
+    a = r.integers(-128, 128, (m, k)).astype(np.int8)
+    w = r.integers(-127, 128, (n, k)).astype(np.int8)
+    ws = r.uniform(1e-3, 1e-2, n).astype(np.float32)
+    bias = r.integers(-20000, 20000, n).astype(np.int32)
+    rc, y = _x86_gemm(a, 0.03, -4, w, ws, bias, 0.75, -1.5, 0.05, 2)
+    assert rc == 0
+    out.update(g_a=a, g_w_nk=w, g_ws=ws, g_bias=bias, g_params=np.float32([0.03, -4, 0.75, -1.5, 0.05, 2]), g_out=y)
+    cases = (("c0", 0, 16, 32, 1, (2, 2), (1, 1), (1, 1), 0), ("c1", 1, 32, 48, 2, (1, 2), (2, 1), (2, 1), -6))
+    for name, layout, c, oc, group, stride, pad, dil, zp in cases:
+        for seed in range(100):
+            rr = np.random.default_rng(0xFEA70105 + 1000 * seed + c)
+            x = rr.integers(-128, 128, (1, c, 18, 22)).astype(np.int8)
+            xl = x if layout == 0 else np.ascontiguousarray(x.transpose(0, 2, 3, 1))
+            wc = rr.integers(-127, 128, (oc, c // group, 3, 3)).astype(np.int8)
+            wcs = rr.uniform(1e-3, 1e-2, oc).astype(np.float32)
+            cb = rr.integers(-3000, 3000, oc).astype(np.int32)
+            rc, yx = _x86_conv(xl, layout, 0.05, zp, wc, group, wcs, cb, stride, pad, dil, 0.4, 3)
+            rco, yo = po.i8_conv2d(xl, 0.05, zp, wc, wcs, cb, stride, pad, 0.4, 3, dilation=dil, group=group,
+                                   layout=layout)
+            if rc == 0 and rco == 0 and np.array_equal(yx, yo):
+                break
+        else:
+            raise RuntimeError(f"no seed with x86 == Common for {name}")
+        out.update({f"{name}_x": xl, f"{name}_w": wc, f"{name}_ws": wcs, f"{name}_bias": cb, f"{name}_out": yx,
+                    f"{name}_geom": np.int32([layout, group, *stride, *pad, *dil, zp])})
+    return out
+
+
 def main():
     R = po.ref()
-    for name, fn in (("codec", make_codec), ("quant", make_quant), ("linear", make_linear), ("argmax", make_argmax)):
+    for name, fn in (("codec", make_codec), ("quant", make_quant), ("linear", make_linear), ("argmax", make_argmax),
+                     ("int8", make_int8)):
         path = os.path.join(HERE, f"{name}.npz")
         np.savez_compressed(path, **fn(R))
         print(f"wrote {path} ({os.path.getsize(path)} bytes)")

@@ -95,3 +95,18 @@ def test_oracle_argmax_matches_golden():
         toks = [po.fp8_gemm_argmax(dtype, g[f"{name}_a"][i], sa, g[f"{name}_w"], sw, s_out)
                 for i in range(g[f"{name}_a"].shape[0])]
         assert toks == g[f"{name}_tokens"].tolist(), name
+
+
+def test_oracle_int8_gemm_and_conv_match_golden():
+    """The reference's x86 INT8 Gemm (zero point, alpha/beta, bias) and Conv2D (NCHW stride 2; NHWC groups
+    and dilation) outputs, bit for bit."""
+    g = golden("int8")
+    s_a, zp_a, alpha, beta, s_out, zp_out = (float(v) for v in g["g_params"])
+    rc, out, _ = po.i8_linear(po.I8_GEMM, g["g_a"], s_a, int(zp_a), g["g_w_nk"], True, g["g_ws"], None, g["g_bias"],
+                              po.BIAS_VECTOR, alpha, beta, s_out, int(zp_out))
+    assert rc == 0 and np.array_equal(out, g["g_out"])
+    for name in ("c0", "c1"):
+        layout, group, sh, sw, ph, pw, dh, dw, zp = (int(v) for v in g[f"{name}_geom"])
+        rc, out = po.i8_conv2d(g[f"{name}_x"], 0.05, zp, g[f"{name}_w"], g[f"{name}_ws"], g[f"{name}_bias"], (sh, sw),
+                               (ph, pw), 0.4, 3, dilation=(dh, dw), group=group, layout=layout)
+        assert rc == 0 and np.array_equal(out, g[f"{name}_out"]), name

@@ -126,3 +126,29 @@ def test_argmax_matches_golden(ctx):
         for i in range(rows):
             ctx.fp8_gemv_argmax(dtype, dev(ac[i:i + 1]), sa, dev(wc), sw, s_out, one)
             assert one.item() == g[f"{name}_tokens"][i], (name, i)
+
+
+def test_i8_gemm_and_conv_match_golden(ctx):
+    """HIP INT8 Gemm and Conv2D against the reference's x86 INT8 kernels' outputs, bit for bit."""
+    g = golden("int8")
+    s_a, zp_a, alpha, beta, s_out, zp_out = (float(v) for v in g["g_params"])
+    a, w = g["g_a"], g["g_w_nk"]
+    m, k = a.shape
+    n = w.shape[0]
+    wt = ctx.prepare_weight(dev(w), po.INT8, k, n, 1, scales=g["g_ws"], version=50)
+    out = torch.empty((m, n), dtype=torch.int8, device="cuda")
+    bias = g["g_bias"]
+    ctx.i8_linear(po.I8_GEMM, dev(a), s_a, int(zp_a), m, wt, out, s_out, int(zp_out), bias=dev(bias),
+                  bias_kind=po.BIAS_VECTOR, bias_abs_max=int(np.abs(bias).max()), alpha=alpha, beta=beta)
+    assert np.array_equal(out.cpu().numpy(), g["g_out"])
+    wt.release()
+    for name in ("c0", "c1"):
+        layout, group, sh, sw, ph, pw, dh, dw, zp = (int(v) for v in g[f"{name}_geom"])
+        cw = ctx.prepare_conv_weight(dev(g[f"{name}_w"]), g[f"{name}_ws"], group=group, version=51)
+        ref = g[f"{name}_out"]
+        y = torch.empty(ref.shape, dtype=torch.int8, device="cuda")
+        cb = g[f"{name}_bias"]
+        ctx.i8_conv2d(dev(g[f"{name}_x"]), layout, 0.05, zp, cw, y, 0.4, 3, stride=(sh, sw), pad=(ph, pw),
+                      dilation=(dh, dw), bias=dev(cb), bias_abs_max=int(np.abs(cb).max()))
+        assert np.array_equal(y.cpu().numpy(), ref), name
+        cw.release()
