@@ -60,3 +60,20 @@ def test_hip_device_enum_and_build_option_patched(patched_tree):
     assert "    HIP\n};" in types
     cmake = (patched_tree / "CMakeLists.txt").read_text()
     assert "FEATHER_ENABLE_HIP" in cmake and "integration/hip_kernels.cc" in cmake
+
+
+def test_adapter_runtime_bookkeeping(tmp_path):
+    """HipExecutionContext's replica and prepared-weight bookkeeping (integration/hip_runtime.cc), built with
+    Feather's own Tensor sources and run on the host against a stand-in of the C ABI
+    (tests/native/adapter_runtime_check.cc): uploads once per host version, outputs stay on the device until
+    read, HostWritten forces a re-upload, persistent replicas survive Release, immutable weights are prepared
+    from their host bytes once, a mutated weight's stale prepared copy is released."""
+    exe = tmp_path / "adapter_check"
+    srcs = [os.path.join(ROOT, "tests", "native", "adapter_runtime_check.cc"), os.path.join(ROOT, "integration",
+                                                                                             "hip_runtime.cc")]
+    srcs += [os.path.join(REF, "src", "core", f) for f in ("tensor.cc", "dim.cc", "memory.cc")]
+    r = subprocess.run(["g++", "-std=c++17", "-O1", f"-I{REF}", f"-I{REF}/include", f"-I{ROOT}/include",
+                        f"-I{ROOT}/integration", *srcs, "-o", str(exe)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-3000:]
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0 and r.stdout.strip() == "OK", r.stdout + r.stderr
