@@ -181,7 +181,8 @@ int fhip_dequantize_linear(fhip_context ctx, const int8_t* src, int64_t count, i
  * For each of m rows (the reference operator takes m = 1; rows are independent): fp32 dot of the
  * BF16 row with every vocabulary row of w [v, k], rounded to BF16; NaN skipped; first strict
  * maximum (lowest index among equal values, +0 == -0); 0 when every value is NaN.
- * logits (optional, [m, v] fp32) receives the fp32 sums. */
+ * logits (optional, [m, v] fp32) receives the fp32 sums.  Rows of up to 64 KiB (K <= 32768), K % 8 == 0,
+ * m <= 16, v < 2^32; otherwise FHIP_ERR_UNSUPPORTED. */
 int fhip_bf16_gemv_argmax(fhip_context ctx, const uint16_t* a, int64_t m, int64_t k, const uint16_t* w, int64_t v,
                           int64_t* tokens, float* logits);
 /* No counterpart in the reference.  For callers that cannot allocate device memory (code under
@@ -196,7 +197,7 @@ int fhip_bf16_gemv_argmax(fhip_context ctx, const uint16_t* a, int64_t m, int64_
 int fhip_bf16_gemv_argmax_noalloc(fhip_context ctx, const uint16_t* a, int64_t m, int64_t k, const uint16_t* w,
                                   int64_t v, int64_t* tokens, float* logits);
 /* FP8 head: Gemm(transB) with out_scale, Cast(fp8 -> bf16), greedy selection
- * (x86/linear_fp8.cc:733-1004; qwen_gemm_argmax_fusion_pass.cc:142-181). */
+ * (x86/linear_fp8.cc:733-1004; qwen_gemm_argmax_fusion_pass.cc:142-181).  K <= 65536, K % 16 == 0. */
 int fhip_fp8_gemv_argmax(fhip_context ctx, int dtype, const uint8_t* a, float a_scale, int64_t m, int64_t k,
                          const uint8_t* w, float w_scale, int64_t v, float out_scale, int64_t* tokens);
 

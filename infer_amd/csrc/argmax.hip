@@ -20,6 +20,8 @@
 #include "codec.h"
 
 #include <algorithm>
+#include <mutex>
+#include <utility>
 
 namespace {
 
@@ -36,7 +38,18 @@ __device__ __forceinline__ uint4 load_stream16(const uint8_t* p) {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kRows = 4;  // weight rows per wave iteration
+constexpr int kRows = 4;  // weight rows per wave and unit of the m = 1 kernel's C5-shaped case (grid sizing)
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [0, N), so register arrays are only ever
+// indexed by constants.
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 __device__ __forceinline__ unsigned long long make_key(uint16_t bf, int64_t idx) {
     if ((bf & 0x7f80u) == 0x7f80u && (bf & 0x7fu) != 0u) return 0ull;  // NaN: never selected
@@ -210,112 +223,198 @@ struct Log2 {
     static constexpr int value = V <= 1 ? 0 : 1 + Log2<V / 2>::value;
 };
 
-template <int KIND, int MT, int kMaxT>
-__global__ __launch_bounds__(kThreads) void gemv_argmax_kernel(const uint8_t* __restrict__ a, int64_t m, int64_t k,
+// ---- m = 1: LDS-ring kernel ------------------------------------------------------------------------
+// Each wave streams units of the weight -- ROWS rows x SEGS 1 KiB segments, one 16-byte load per lane
+// per row segment, 8 loads in all -- into its own two-slot LDS ring with buffer_load ... lds (no VGPR
+// round trip), and computes unit u while unit u+1 is in flight.  A wave walks row groups g = gw,
+// gw + GW, ... (gw its global wave index, GW the wave count), each group being nsb consecutive units
+// over the row's segments; the per-lane partial sums of the group's ROWS rows carry across its units
+// and are reduced (transposing butterfly) after the last one.
+// Measured against the register double buffer this replaces (C5 head, 311 MB): ~4 us less per call.
+// One strip in flight per wave (two slots) is the fastest depth: more slots put more of the head in
+// flight than the HBM system serves best (three or four slots measured slower).
+// The activation stays in registers when one unit covers the whole row (WHOLE), and otherwise sits in
+// LDS behind the rings, zero-padded to whole units, so any K with K * esize <= kArgmaxMaxRowBytes works.
+// Lanes past the row's end and rows past v load out of the buffer resource's range, which writes zeros
+// into the ring without touching memory.
+typedef __attribute__((address_space(3))) void* lds_ptr;
+constexpr int kRingSlots = 2;
+constexpr int kUnitLoads = 8;                      // 1 KiB wave loads per unit
+constexpr int kUnitBytes = kUnitLoads * 1024;
+constexpr int kRingBytes = kWaves * kRingSlots * kUnitBytes;  // 64 KiB
+constexpr int kBufferRsrcWord3 = 0x00020000;       // raw byte-addressed buffer
+constexpr int kCachePolicyNT = 2;                  // non-temporal: the head streams once
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    // gfx9 s_waitcnt: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[15:14]
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | (((N >> 4) & 3) << 14));
+}
+
+// LDS read as inline asm: the compiler's wait-count pass would otherwise treat it as aliasing the
+// in-flight LDS-DMA loads and drain them all (vmcnt(0)) in front of it.  The caller orders it with
+// wait_vmcnt and waits for it with lgkmcnt(0).
+template <int OFF>
+__device__ __forceinline__ u32x4 lds_read16(uint32_t addr) {
+    u32x4 v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    return v;
+}
+
+__device__ __forceinline__ uint4 to_uint4(const u32x4& v) { return make_uint4(v.x, v.y, v.z, v.w); }
+
+template <int KIND, int ROWS, int SEGS, bool WHOLE>
+__global__ __launch_bounds__(kThreads) void gemv_argmax_kernel(const uint8_t* __restrict__ a, int64_t k,
                                                                const uint8_t* __restrict__ w, int64_t v,
                                                                HeadParams hp, unsigned long long* __restrict__ partials,
                                                                ArgmaxScratch* __restrict__ scratch,
                                                                int64_t* __restrict__ tokens) {
+    static_assert(ROWS * SEGS == kUnitLoads, "a unit is kUnitLoads row segments");
     using H = Head<KIND>;
     constexpr int esize = KIND == 0 ? 2 : 1;
-    constexpr int V = kRows * MT;                 // values reduced per wave iteration
-    constexpr int kShift = 6 - Log2<V>::value;
+    constexpr int kShift = 6 - Log2<ROWS>::value;
+    extern __shared__ __align__(16) uint8_t smem[];  // [kWaves][kRingSlots][kUnitBytes] rings, then the activation
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t row_bytes = k * esize;
-    const int64_t chunks = row_bytes / 16;  // host guarantees k * esize % 16 == 0
-    // Activation chunks this lane covers: c = lane + 64*t, t < kMaxT (k * esize <= kMaxT KiB).
-    uint4 xa[MT][kMaxT];
-#pragma unroll
-    for (int j = 0; j < MT; ++j)
-#pragma unroll
-        for (int t = 0; t < kMaxT; ++t) {
-            const int64_t c = lane + 64 * t;
-            xa[j][t] = (j < m && c < chunks) ? *reinterpret_cast<const uint4*>(a + j * row_bytes + c * 16)
-                                             : make_uint4(0, 0, 0, 0);
-        }
-    // After the transposing reduction this lane owns value index my_idx = r * MT + j.
-    const int my_idx = lane >> kShift;
-    const int my_r = my_idx / MT, my_j = my_idx % MT;
-    const bool writer = (lane & ((1 << kShift) - 1)) == 0;
-    unsigned long long best = 0ull;
+    const int nsb = WHOLE ? 1 : (int)((row_bytes + SEGS * 1024 - 1) / (SEGS * 1024));  // units per row group
+    uint8_t* const ring = smem + wave * (kRingSlots * kUnitBytes);
+    const uint32_t ring_addr = (uint32_t)(uintptr_t)(lds_ptr)ring + (uint32_t)lane * 16u;
+    uint8_t* const xl = smem + kRingBytes;
+    const uint32_t x_addr = (uint32_t)(uintptr_t)(lds_ptr)xl + (uint32_t)lane * 16u;
 
-    const int64_t stride = (int64_t)gridDim.x * kWaves * kRows;
-    // Register double buffer: the next strip of rows is requested before the current one is used.
-    uint4 wv[kMaxT][kRows], wn[kMaxT][kRows];
-    auto load_rows = [&](int64_t first, uint4 (&dst)[kMaxT][kRows]) {
+    float xf[WHOLE ? SEGS : 1][H::kPer16];
+    if constexpr (WHOLE) {
 #pragma unroll
-        for (int t = 0; t < kMaxT; ++t) {
-            const int64_t c = lane + 64 * t;
-            if (c < chunks) {
+        for (int j = 0; j < SEGS; ++j) {
+            const int64_t col = (int64_t)j * 1024 + lane * 16;
+            const uint4 c = col < row_bytes ? *reinterpret_cast<const uint4*>(a + col) : make_uint4(0, 0, 0, 0);
+            H::decode(c, xf[j]);
+        }
+    } else {
+        const int64_t padded = (int64_t)nsb * SEGS * 1024;
+        for (int64_t c = (int64_t)threadIdx.x * 16; c < padded; c += kThreads * 16)
+            *reinterpret_cast<uint4*>(xl + c) = c < row_bytes ? *reinterpret_cast<const uint4*>(a + c) : make_uint4(0, 0, 0, 0);
+        __syncthreads();
+    }
+
+    const int64_t gw = (int64_t)blockIdx.x * kWaves + wave;
+    const int64_t group_stride = (int64_t)gridDim.x * kWaves * ROWS;
+    // Issue side: the unit (i_row, i_b) goes to slot i_slot; one unit ahead of the compute side.
+    int64_t i_row = gw * ROWS;
+    int i_b = 0, i_slot = 0;
+    auto issue = [&]() {
+        const bool live = i_row < v;
+        const int64_t rem = live ? (v - i_row) * row_bytes : 0;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(w + (live ? i_row : 0) * row_bytes), 0, (int)(rem < 0x7fffffff ? rem : 0x7fffffff), kBufferRsrcWord3);
+        uint8_t* const dst = ring + i_slot * kUnitBytes;
 #pragma unroll
-                for (int r = 0; r < kRows; ++r) {
-                    const int64_t row = first + r < v ? first + r : v - 1;
-                    dst[t][r] = load_stream16(w + row * row_bytes + c * 16);
-                }
+        for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+            for (int j = 0; j < SEGS; ++j) {
+                const int64_t col = (int64_t)(i_b * SEGS + j) * 1024 + lane * 16;
+                const uint32_t off = col < row_bytes ? (uint32_t)(r * row_bytes + col) : 0x80000000u;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(dst + (r * SEGS + j) * 1024), 16, off, 0, 0,
+                                                         kCachePolicyNT);
             }
+        i_slot ^= 1;
+        if (++i_b == nsb) {
+            i_b = 0;
+            i_row += group_stride;
         }
     };
-    int64_t r0 = ((int64_t)blockIdx.x * kWaves + wave) * kRows;
-    if (r0 < v) load_rows(r0, wv);
-    for (; r0 < v; r0 += stride) {
-        if (r0 + stride < v) load_rows(r0 + stride, wn);
-        float acc[V];
-#pragma unroll
-        for (int i = 0; i < V; ++i) acc[i] = 0.0f;
-#pragma unroll
-        for (int t = 0; t < kMaxT; ++t) {
-            const int64_t c = lane + 64 * t;
-            if (c < chunks) {
-                float wf[kRows][H::kPer16];
-#pragma unroll
-                for (int r = 0; r < kRows; ++r) H::decode(wv[t][r], wf[r]);
-#pragma unroll
-                for (int j = 0; j < MT; ++j) {
-                    float xf[H::kPer16];
-                    H::decode(xa[j][t], xf);
-#pragma unroll
-                    for (int r = 0; r < kRows; ++r) {
-                        float s = acc[r * MT + j];
-#pragma unroll
-                        for (int i = 0; i < H::kPer16; ++i) s += xf[i] * wf[r][i];
-                        acc[r * MT + j] = s;
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < kMaxT; ++t)
-#pragma unroll
-            for (int r = 0; r < kRows; ++r) wv[t][r] = wn[t][r];
-        float s = transpose_reduce<V>(acc, lane);
-        const int64_t row = r0 + my_r;
-        if (row < v && my_j < m) {
-            uint16_t bf;
-            if constexpr (KIND == 0) {
-                bf = fhip::bf16_encode(s);
-            } else {
-                const uint8_t code = fhip::fp8_encode(s * hp.ab_scale / hp.out_scale, KIND == 2);
-                s = fhip::fp8_decode(code, KIND == 2) * hp.out_scale;
-                bf = fhip::bf16_encode(s);
-            }
-            const unsigned long long key = make_key(bf, row);
-            best = key > best ? key : best;
-            if (hp.logits != nullptr && writer) hp.logits[my_j * v + row] = s;
-        }
-    }
 
-    // Block reduction -> partials[block][j]
-    __shared__ unsigned long long red[kWaves * 64];
-    red[threadIdx.x] = best;
-    __syncthreads();
-    if (threadIdx.x < MT) {
-        unsigned long long b = 0ull;
-        for (int q = 0; q < kWaves * 64; ++q)
-            if (((q & 63) >> kShift) % MT == (int)threadIdx.x) b = red[q] > b ? red[q] : b;
-        publish_key(&partials[(int64_t)blockIdx.x * MT + threadIdx.x], b);
+    unsigned long long best = 0ull;
+    float acc[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
+    int64_t c_row = gw * ROWS;
+    int c_b = 0, c_slot = 0;
+    issue();
+    while (c_row < v) {
+        wait_vmcnt<0>();  // this unit has landed; nothing else is in flight
+        issue();          // the next unit goes to the other slot, whose reads completed last iteration
+        const uint32_t sa = ring_addr + (uint32_t)(c_slot * kUnitBytes);
+        u32x4 wv[ROWS][SEGS];
+        static_for<ROWS * SEGS>([&](auto ii) {
+            constexpr int i = decltype(ii)::value;
+            wv[i / SEGS][i % SEGS] = lds_read16<i * 1024>(sa);
+        });
+        u32x4 xv[WHOLE ? 1 : SEGS];
+        if constexpr (!WHOLE) {
+            const uint32_t xa = x_addr + (uint32_t)(c_b * SEGS * 1024);
+            static_for<SEGS>([&](auto jj) {
+                constexpr int j = decltype(jj)::value;
+                xv[j] = lds_read16<j * 1024>(xa);
+            });
+        }
+        // Wait for the reads, and tie every fragment register to the wait so no use of one is scheduled above it.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+            for (int j = 0; j < SEGS; ++j) asm volatile("" : "+v"(wv[r][j]));
+        if constexpr (!WHOLE) {
+#pragma unroll
+            for (int j = 0; j < SEGS; ++j) asm volatile("" : "+v"(xv[j]));
+        }
+#pragma unroll
+        for (int j = 0; j < SEGS; ++j) {
+            float xs[H::kPer16];
+            if constexpr (WHOLE) {
+#pragma unroll
+                for (int i = 0; i < H::kPer16; ++i) xs[i] = xf[j][i];
+            } else {
+                H::decode(to_uint4(xv[j]), xs);
+            }
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                float wf[H::kPer16];
+                H::decode(to_uint4(wv[r][j]), wf);
+                float s = acc[r];
+#pragma unroll
+                for (int i = 0; i < H::kPer16; ++i) s += xs[i] * wf[i];
+                acc[r] = s;
+            }
+        }
+        c_slot ^= 1;
+        if (++c_b == nsb) {
+            c_b = 0;
+            float s = transpose_reduce<ROWS>(acc, lane);
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
+            const int64_t row = c_row + (lane >> kShift);
+            if (row < v) {
+                uint16_t bf;
+                if constexpr (KIND == 0) {
+                    bf = fhip::bf16_encode(s);
+                } else {
+                    const uint8_t code = fhip::fp8_encode(s * hp.ab_scale / hp.out_scale, KIND == 2);
+                    s = fhip::fp8_decode(code, KIND == 2) * hp.out_scale;
+                    bf = fhip::bf16_encode(s);
+                }
+                const unsigned long long key = make_key(bf, row);
+                best = key > best ? key : best;
+                if (hp.logits != nullptr && (lane & ((1 << kShift) - 1)) == 0) hp.logits[row] = s;
+            }
+            c_row += group_stride;
+        }
     }
-    ticket_and_finish<MT, true>(partials, m, scratch, tokens);
+    wait_vmcnt<0>();  // the trailing unit (past the end: zeros, no memory traffic) lands before the wave exits
+
+    // Block reduction -> partials[block]
+    __shared__ unsigned long long red[kWaves];
+    best = wave_max(best);
+    if (lane == 0) red[wave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long b = red[0];
+#pragma unroll
+        for (int q = 1; q < kWaves; ++q) b = red[q] > b ? red[q] : b;
+        publish_key(&partials[blockIdx.x], b);
+    }
+    ticket_and_finish<1, true>(partials, 1, scratch, tokens);
 }
 
 // ---- m >= 2: MFMA kernel --------------------------------------------------------------------------
@@ -487,19 +586,39 @@ int launch_on(hipStream_t stream, const Plan& plan, const uint8_t* a, int64_t m,
         FHIP_ARGMAX_MFMA_CASE(KIND == 0 ? 16 : 8)
 #undef FHIP_ARGMAX_MFMA_CASE
     }
-    const int t = bytes <= 1024 ? 1 : (bytes <= 2048 ? 2 : 4);
-#define FHIP_ARGMAX_CASE(MT, T)                                                                              \
-    if (m <= MT && t == T) {                                                                                 \
-        gemv_argmax_kernel<KIND, MT, T><<<(unsigned)plan.grid1, kThreads, 0, stream>>>(a, m, k, w, v, hp,    \
-                                                                                   partials, tickets, tokens); \
-        *err = hipGetLastError();                                                                            \
-        return *err == hipSuccess ? FHIP_OK : FHIP_ERR_HIP;                                                  \
+    // m = 1 (and rows beyond the MFMA kernel's K, one launch per activation row): the LDS-ring kernel.
+    // Unit shape: 4 rows x 2 segments when the row is 1-2 KiB (the C5 head), else 8 rows x 1 segment.
+    const int64_t nseg = (bytes + 1023) / 1024;
+    for (int64_t j = 0; j < m; ++j) {
+        const uint8_t* aj = a + j * bytes;
+        HeadParams hpj = hp;
+        if (hp.logits) hpj.logits = hp.logits + j * v;
+        if (nseg == 2) {
+            gemv_argmax_kernel<KIND, 4, 2, true><<<(unsigned)plan.grid1, kThreads, kRingBytes, stream>>>(
+                aj, k, w, v, hpj, partials, tickets, tokens + j);
+        } else if (nseg == 1) {
+            gemv_argmax_kernel<KIND, 8, 1, true><<<(unsigned)plan.grid1, kThreads, kRingBytes, stream>>>(
+                aj, k, w, v, hpj, partials, tickets, tokens + j);
+        } else {
+            const size_t lds = (size_t)kRingBytes + (size_t)nseg * 1024;
+            static std::once_flag once;
+            static hipError_t attr = hipSuccess;
+            std::call_once(once, [] {
+                attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_argmax_kernel<KIND, 8, 1, false>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           kRingBytes + kArgmaxMaxRowBytes);
+            });
+            if (attr != hipSuccess) {
+                *err = attr;
+                return FHIP_ERR_HIP;
+            }
+            gemv_argmax_kernel<KIND, 8, 1, false><<<(unsigned)plan.grid1, kThreads, lds, stream>>>(
+                aj, k, w, v, hpj, partials, tickets, tokens + j);
+        }
+        *err = hipGetLastError();
+        if (*err != hipSuccess) return FHIP_ERR_HIP;
     }
-    FHIP_ARGMAX_CASE(1, 1)
-    FHIP_ARGMAX_CASE(1, 2)
-    FHIP_ARGMAX_CASE(1, 4)
-#undef FHIP_ARGMAX_CASE
-    return FHIP_ERR_UNSUPPORTED;
+    return FHIP_OK;
 }
 
 template <int KIND>
@@ -596,8 +715,8 @@ int check_bf16_args(fhip_context ctx, const uint16_t* a, int64_t m, int64_t k, c
         return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, std::string(fn) + ": empty K or vocabulary");
     if (!a || !w || !tokens || m < 0 || k < 0 || v < 0)
         return fhip::set_error(ctx, FHIP_ERR_INVALID, std::string(fn) + ": bad arguments");
-    if (m > kArgmaxMaxRows || (k * 2) % 16 != 0 || k * 2 > 4096 || v >= (int64_t(1) << 32))
-        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, std::string(fn) + ": needs m <= 16, k % 8 == 0, k <= 2048");
+    if (m > kArgmaxMaxRows || (k * 2) % 16 != 0 || k * 2 > kArgmaxMaxRowBytes || v >= (int64_t(1) << 32))
+        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, std::string(fn) + ": needs m <= 16, k % 8 == 0, k <= 32768");
     if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(w)) & 15)
         return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, std::string(fn) + ": pointers must be 16-byte aligned");
     return FHIP_OK;
@@ -635,8 +754,8 @@ int fhip_fp8_gemv_argmax(fhip_context ctx, int dtype, const uint8_t* a, float a_
         return fhip::set_error(ctx, FHIP_ERR_INVALID, "fp8_gemv_argmax: bad arguments");
     if (!fhip::valid_scale(a_scale) || !fhip::valid_scale(w_scale) || !fhip::valid_scale(out_scale))
         return fhip::set_error(ctx, FHIP_ERR_INVALID, "fp8_gemv_argmax: scales must be finite and positive");
-    if (m > kArgmaxMaxRows || k % 16 != 0 || k > 4096 || v >= (int64_t(1) << 32))
-        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "fp8_gemv_argmax: needs m <= 16, k % 16 == 0, k <= 4096");
+    if (m > kArgmaxMaxRows || k % 16 != 0 || k > kArgmaxMaxRowBytes || v >= (int64_t(1) << 32))
+        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "fp8_gemv_argmax: needs m <= 16, k % 16 == 0, k <= 65536");
     if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(w)) & 15)
         return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "fp8_gemv_argmax: pointers must be 16-byte aligned");
     HeadParams hp{a_scale * w_scale, out_scale, nullptr};

@@ -16,6 +16,9 @@
 // address takes an atomic from every block.  Each counter has its own 128-byte line.  Every kernel
 // that uses them leaves them zeroed on exit, so calls and graph replays need no memset.
 constexpr int kArgmaxMaxRows = 16;
+// Longest LM-head row (K * element size) the argmax kernels take: the m = 1 kernel keeps the activation
+// row in LDS beside its weight rings.
+constexpr int kArgmaxMaxRowBytes = 65536;
 constexpr int kTicketGroups = 32;
 struct ArgmaxScratch {
     unsigned int done;

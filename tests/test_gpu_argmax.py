@@ -121,6 +121,36 @@ def test_bf16_argmax_mfma_shapes(ctx, m, k):
         assert np.max(np.abs(lg[j] - ref)) <= 1e-2 * np.max(np.abs(ref))
 
 
+@pytest.mark.parametrize("m,k", [(1, 256), (1, 512), (1, 1032), (1, 3584), (1, 8192), (2, 3584), (1, 32768)])
+def test_bf16_argmax_row_lengths(ctx, m, k):
+    """The m = 1 kernel's unit shapes: rows of one segment (K = 256: half a segment, 512: one) and of two
+    (the C5 shape, covered above), and rows over several segment blocks with the activation in LDS (K =
+    1032: a 16-byte last segment; 3584: the Qwen 7B hidden size; 8192; 32768, the longest row taken).
+    m = 2 at K = 3584 is past the MFMA kernel's K and runs the m = 1 kernel once per row.  V = 20011
+    ends in a partial row group; the logits are checked too."""
+    v = 20011 if k <= 8192 else 3001
+    a, w = head_inputs(SEEDS[5] + 11 * m + k, m, k, v)
+    tokens = torch.empty(m, dtype=torch.int64, device="cuda")
+    logits = torch.empty((m, v), dtype=torch.float32, device="cuda")
+    ctx.bf16_gemv_argmax(dev(a), dev(w), tokens, logits)
+    assert check_tokens(a, w, tokens.cpu().numpy()) == 0
+    lg = logits.cpu().numpy()
+    for j in range(m):
+        _, ref = po.bf16_gemm_argmax(a[j], w, want_logits=True)
+        assert np.max(np.abs(lg[j] - ref)) <= 1e-2 * np.max(np.abs(ref))
+
+
+def test_bf16_argmax_rejects_longer_rows(ctx):
+    """Rows beyond 64 KiB (K > 32768 BF16) are refused with FHIP_ERR_UNSUPPORTED, not computed wrongly."""
+    from infer_amd.runtime import FhipError
+    k, v = 32776, 64
+    a = torch.zeros((1, k), dtype=torch.int16, device="cuda")
+    w = torch.zeros((v, k), dtype=torch.int16, device="cuda")
+    tokens = torch.empty(1, dtype=torch.int64, device="cuda")
+    with pytest.raises(FhipError):
+        ctx.bf16_gemv_argmax(a, w, tokens)
+
+
 def test_bf16_argmax_repeated_calls_rearm(ctx):
     """The completion ticket re-arms itself: back-to-back calls with different data stay correct."""
     k, v = 512, 5000
@@ -132,7 +162,7 @@ def test_bf16_argmax_repeated_calls_rearm(ctx):
 
 
 @pytest.mark.parametrize("dtype", [po.FP8E4M3, po.FP8E5M2])
-@pytest.mark.parametrize("m,k", [(1, 1024), (5, 1024), (3, 4096)])
+@pytest.mark.parametrize("m,k", [(1, 1024), (5, 1024), (3, 4096), (1, 512), (1, 6144), (2, 8192)])
 def test_fp8_argmax_head(ctx, dtype, m, k):
     from tests.common import fp8_tensor, fp8_pow2_scale
     v = 32768
