@@ -421,34 +421,48 @@ __global__ __launch_bounds__(kThreads) void gemv_argmax_kernel(const uint8_t* __
 // A block walks vocabulary tiles of 16 rows (grid-stride).  Its 4 waves split K: wave w owns the
 // SPW consecutive steps starting at w*SPW, a step being 32 BF16 (v_mfma_f32_16x16x32_bf16) or 128 FP8
 // (v_mfma_scale_f32_16x16x128_f8f6f4, unit scales) values of K.  The activation rows are the A operand
-// and stay in registers for the whole kernel; each tile's weight rows are the B operand, loaded
-// straight from HBM, and the next tile's loads are issued before the current tile is reduced.  Lane
-// l supplies row l%16 (activation row / vocabulary row) and the l/16-th 16-byte (BF16) or 32-byte
-// (FP8) slice of the step, for A and B alike.  The four partial 16x16 tiles meet in LDS (double
-// buffered: one barrier per tile) and thread t finishes activation row t/16 of vocabulary row t%16.
+// and stay in registers for the whole kernel; each tile's weight rows are the B operand.  Each wave
+// streams its own K quarter of the tile (16 rows x SPW steps) into a private two-slot LDS ring with
+// 1 KiB buffer_load ... lds loads and computes one tile while the next is in flight, so the ring needs
+// no barrier (measured on the C5 head, M = 8: 54.4 us against 62.3 us for the same kernel loading B
+// into registers with a register double buffer).  The lanes of a DMA load are permuted so that LDS
+// holds each row's chunks XOR-swizzled by the row index, and the fragment reads of 16 rows x one
+// chunk hit 16 distinct bank groups.  Lane l supplies row l%16 (activation row / vocabulary row) and
+// the l/16-th 16-byte (BF16) or 32-byte (FP8) slice of the step, for A and B alike.  The four partial
+// 16x16 tiles meet in LDS (double buffered: one barrier per tile) and thread t finishes activation
+// row t/16 of vocabulary row t%16.
+
+// Dynamic LDS of the MFMA kernel: each wave's two-slot ring of its K quarter of a 16-row tile.
+template <int KIND, int SPW>
+constexpr size_t mfma_ring_bytes() {
+    return (size_t)kWaves * 2 * 16 * SPW * 4 * (KIND == 0 ? 16 : 32);
+}
+
 template <int KIND, int SPW>
 __global__ __launch_bounds__(kThreads) void gemv_argmax_mfma_kernel(const uint8_t* __restrict__ a, int64_t m,
-                                                                    int64_t k, const uint8_t* __restrict__ w,
-                                                                    int64_t v, HeadParams hp,
-                                                                    unsigned long long* __restrict__ partials,
-                                                                    ArgmaxScratch* __restrict__ scratch,
-                                                                    int64_t* __restrict__ tokens) {
+                                                                         int64_t k, const uint8_t* __restrict__ w,
+                                                                         int64_t v, HeadParams hp,
+                                                                         unsigned long long* __restrict__ partials,
+                                                                         ArgmaxScratch* __restrict__ scratch,
+                                                                         int64_t* __restrict__ tokens) {
     constexpr int esize = KIND == 0 ? 2 : 1;
-    constexpr int SB = KIND == 0 ? 16 : 32;  // bytes per lane per step
-    constexpr int NV = SB / 16;              // 16-byte loads per lane per step
+    constexpr int SB = KIND == 0 ? 16 : 32;   // bytes per lane per step
+    constexpr int NV = SB / 16;               // 16-byte fragment reads per lane per step
+    constexpr int QB = SPW * 4 * SB;          // bytes of each row in one wave's K quarter
+    constexpr int CPR = QB / 16;              // 16-byte chunks per row of a quarter
+    constexpr int SWM = (CPR < 16 ? CPR : 16) - 1;
+    constexpr int QBYTES = 16 * QB;           // one wave's quarter of a 16-row tile
+    constexpr int LOADS = QBYTES / 1024;      // 1 KiB DMA loads per wave per tile
+    static_assert(QBYTES % 1024 == 0, "a quarter is whole 1 KiB loads");
+    static_assert(LOADS <= 32, "vmcnt range");
+    extern __shared__ __align__(16) uint8_t smem[];  // [kWaves][2 slots][QBYTES]
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int fr = lane & 15;
     const int64_t row_bytes = k * esize;
-    // this lane's byte offsets in a row, one per step; slices past the row read byte 0 and are zeroed
-    int64_t off[SPW];
-    bool live[SPW];
-#pragma unroll
-    for (int s = 0; s < SPW; ++s) {
-        const int64_t o = (int64_t)(wave * SPW + s) * (4 * SB) + (lane >> 4) * SB;
-        live[s] = o < row_bytes;
-        off[s] = live[s] ? o : 0;
-    }
+    const int64_t qoff = (int64_t)wave * QB;  // this wave's quarter within a row
+    uint8_t* const ring = smem + wave * 2 * QBYTES;
+    // activation fragments (A operand), masked past the row end and past m
     uint4 xa[SPW][NV];
     {
         const bool arow = fr < m;
@@ -457,51 +471,86 @@ __global__ __launch_bounds__(kThreads) void gemv_argmax_mfma_kernel(const uint8_
         for (int s = 0; s < SPW; ++s)
 #pragma unroll
             for (int q = 0; q < NV; ++q) {
-                // masked, not selected: a select lets the compiler branch around each load and wait for
-                // it inside the branch, serializing the activation loads
-                const uint4 x = *reinterpret_cast<const uint4*>(ar + off[s] + 16 * q);
-                const uint32_t msk = (arow && live[s]) ? 0xffffffffu : 0u;
+                const int64_t o = qoff + s * 4 * SB + (lane >> 4) * SB + 16 * q;
+                const bool live = arow && o < row_bytes;
+                const uint4 x = *reinterpret_cast<const uint4*>(ar + (live ? o : 0));
+                const uint32_t msk = live ? 0xffffffffu : 0u;
                 xa[s][q] = make_uint4(x.x & msk, x.y & msk, x.z & msk, x.w & msk);
             }
     }
+    // DMA lane map: load i, lane p fills LDS chunk f = i*64 + p of the quarter ([row][CPR] chunks), which
+    // holds chunk (f % CPR) ^ swz(row) of that row, so the fragment reads of 16 rows x one chunk hit 16
+    // distinct bank groups.
+    uint32_t voff[LOADS];
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+        const int f = i * 64 + lane;
+        const int row = f / CPR;
+        const int c = (f % CPR) ^ (row & SWM);
+        const int64_t col = qoff + c * 16;
+        voff[i] = col < row_bytes ? (uint32_t)(row * row_bytes + col) : 0x80000000u;
+    }
     const int64_t ntiles = (v + 15) / 16;
-    uint4 wv[SPW][NV], wn[SPW][NV];
-    auto load_tile = [&](int64_t tile, uint4 (&dst)[SPW][NV]) {
-        int64_t row = tile * 16 + fr;
-        row = row < v ? row : v - 1;
-        const uint8_t* wr = w + row * row_bytes;
+    auto issue = [&](int64_t t_issue, int s_issue) {
+        const bool live = t_issue < ntiles;
+        const int64_t row0 = live ? t_issue * 16 : 0;
+        const int64_t rem = live ? (v - row0) * row_bytes : 0;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(w + row0 * row_bytes), 0, (int)(rem < 0x7fffffff ? rem : 0x7fffffff), kBufferRsrcWord3);
+        uint8_t* const dst = ring + s_issue * QBYTES;
 #pragma unroll
-        for (int s = 0; s < SPW; ++s)
-#pragma unroll
-            for (int q = 0; q < NV; ++q) dst[s][q] = load_stream16(wr + off[s] + 16 * q);
+        for (int i = 0; i < LOADS; ++i) {
+            const uint32_t off = voff[i];
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(dst + i * 1024), 16, off, 0, 0, kCachePolicyNT);
+        }
     };
+    // fragment read addresses: row fr, chunk s*(4*SB/16) + (lane>>4)*NV + q
+    const uint32_t rbase = (uint32_t)(uintptr_t)(lds_ptr)ring + (uint32_t)(fr * CPR * 16);
+    uint32_t rcol[SPW][NV];
+#pragma unroll
+    for (int s = 0; s < SPW; ++s)
+#pragma unroll
+        for (int q = 0; q < NV; ++q) rcol[s][q] = (uint32_t)((((s * 4 * SB) / 16 + (lane >> 4) * NV + q) ^ (fr & SWM)) * 16);
     __shared__ float red[2][kWaves][16][17];
     const int my_m = threadIdx.x >> 4, my_c = threadIdx.x & 15;
     unsigned long long best = 0ull;
-    int buf = 0;
+    int buf = 0, slot = 0;
     int64_t tile = blockIdx.x;
-    if (tile < ntiles) load_tile(tile, wv);
+    issue(tile, 0);
     for (; tile < ntiles; tile += gridDim.x) {
-        if (tile + gridDim.x < ntiles) load_tile(tile + gridDim.x, wn);
+        wait_vmcnt<0>();
+        issue(tile + gridDim.x, slot ^ 1);
+        const uint32_t sb = rbase + (uint32_t)(slot * QBYTES);
+        u32x4 bw[SPW][NV];
+#pragma unroll
+        for (int s = 0; s < SPW; ++s)
+#pragma unroll
+            for (int q = 0; q < NV; ++q) {
+                u32x4 t;
+                asm volatile("ds_read_b128 %0, %1" : "=v"(t) : "v"(sb + rcol[s][q]));
+                bw[s][q] = t;
+            }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int s = 0; s < SPW; ++s)
+#pragma unroll
+            for (int q = 0; q < NV; ++q) asm volatile("" : "+v"(bw[s][q]));
         v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int s = 0; s < SPW; ++s) {
-            uint4 b0 = wv[s][0];
-            if (!live[s]) b0 = make_uint4(0, 0, 0, 0);
             if constexpr (KIND == 0) {
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xa[s][0]), __builtin_bit_cast(v8bf, b0),
-                                                              acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xa[s][0]),
+                                                              __builtin_bit_cast(v8bf, bw[s][0]), acc, 0, 0, 0);
             } else {
-                uint4 b1 = wv[s][NV - 1];
-                if (!live[s]) b1 = make_uint4(0, 0, 0, 0);
                 const v8i av = v8i{(int)xa[s][0].x, (int)xa[s][0].y, (int)xa[s][0].z, (int)xa[s][0].w,
                                    (int)xa[s][NV - 1].x, (int)xa[s][NV - 1].y, (int)xa[s][NV - 1].z, (int)xa[s][NV - 1].w};
-                const v8i bv = v8i{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+                const v8i bv = v8i{(int)bw[s][0].x, (int)bw[s][0].y, (int)bw[s][0].z, (int)bw[s][0].w,
+                                   (int)bw[s][NV - 1].x, (int)bw[s][NV - 1].y, (int)bw[s][NV - 1].z, (int)bw[s][NV - 1].w};
                 acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc, KIND == 2 ? 1 : 0, KIND == 2 ? 1 : 0,
                                                                       0, 127, 0, 127);
             }
         }
-        // C fragment of lane l: vocabulary row l%16 of the tile, activation rows 4*(l/16) .. +3.
+        slot ^= 1;
 #pragma unroll
         for (int r = 0; r < 4; ++r) red[buf][wave][(lane >> 4) * 4 + r][fr] = acc[r];
         __syncthreads();
@@ -521,18 +570,13 @@ __global__ __launch_bounds__(kThreads) void gemv_argmax_mfma_kernel(const uint8_
             if (hp.logits != nullptr) hp.logits[my_m * v + row] = sum;
         }
         buf ^= 1;
-#pragma unroll
-        for (int s = 0; s < SPW; ++s)
-#pragma unroll
-            for (int q = 0; q < NV; ++q) wv[s][q] = wn[s][q];
     }
-    // 16 consecutive threads share an activation row: reduce within the group, one key per row.
+    wait_vmcnt<0>();
 #pragma unroll
     for (int o = 8; o > 0; o >>= 1) {
         const unsigned long long x = __shfl_xor(best, o, 64);
         best = x > best ? x : best;
     }
-    // keys leave through wave 0 (threads 0..15), whose own wait covers them before the ticket
     __shared__ unsigned long long row_key[16];
     if (my_c == 0) row_key[my_m] = best;
     __syncthreads();
@@ -575,7 +619,20 @@ int launch_on(hipStream_t stream, const Plan& plan, const uint8_t* a, int64_t m,
         const int64_t spw_need = ((bytes + step_bytes - 1) / step_bytes + kWaves - 1) / kWaves;
 #define FHIP_ARGMAX_MFMA_CASE(SPW)                                                                              \
         if (spw_need <= (SPW)) {                                                                                \
-            gemv_argmax_mfma_kernel<KIND, SPW><<<(unsigned)plan.mgrid, kThreads, 0, stream>>>(a, m, k, w, v, hp, \
+            constexpr size_t lds = mfma_ring_bytes<KIND, SPW>();                                                \
+            if (lds > 65536) {                                                                                  \
+                static std::once_flag once;                                                                     \
+                static hipError_t attr = hipSuccess;                                                            \
+                std::call_once(once, [] {                                                                       \
+                    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_argmax_mfma_kernel<KIND, SPW>), \
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);           \
+                });                                                                                             \
+                if (attr != hipSuccess) {                                                                       \
+                    *err = attr;                                                                                \
+                    return FHIP_ERR_HIP;                                                                        \
+                }                                                                                               \
+            }                                                                                                   \
+            gemv_argmax_mfma_kernel<KIND, SPW><<<(unsigned)plan.mgrid, kThreads, lds, stream>>>(a, m, k, w, v, hp, \
                                                                                  partials, tickets, tokens);    \
             *err = hipGetLastError();                                                                           \
             return *err == hipSuccess ? FHIP_OK : FHIP_ERR_HIP;                                                 \
