@@ -198,6 +198,30 @@ def test_i8_conv_config4_bitexact(ctx, pow2):
     wt.release()
 
 
+@pytest.mark.parametrize("sign", [1, -1])
+def test_i8_conv_requant_near_ties(ctx, sign):
+    """The conv epilogue's requantization on values just off an x.5 point: with s_in * s_w / s_out =
+    0.5 + 2^-21 every odd sum x lands x * 2^-21 (<= 1.2e-4) above or below a tie; the reference rounds each
+    away from the tie, and so must the reciprocal-multiply fast path with its division fallback
+    (requant_i8).  Small operands keep most sums inside the int8 range."""
+    r = rng(77)
+    n, c, h, wd, oc = 1, 64, 9, 32, 16
+    x = r.integers(-2, 3, (n, c, h, wd)).astype(np.int8)
+    w = (sign * r.integers(-2, 3, (oc, c, 3, 3))).astype(np.int8)
+    s_w = np.full(oc, np.float32(0.5 + 2.0 ** -21), np.float32)
+    rc, ref = po.i8_conv2d(x, 1.0, 0, w, s_w, None, 1, 1, 1.0, 0)
+    assert rc == 0
+    wt = ctx.prepare_conv_weight(dev(w), s_w, version=7)
+    out = torch.empty(ref.shape, dtype=torch.int8, device="cuda")
+    ctx.i8_conv2d(dev(x), 0, 1.0, 0, wt, out, 1.0, 0, stride=(1, 1), pad=(1, 1))
+    assert ctx.last_backend() == "i8_mfma_conv_window"
+    got = out.cpu().numpy()
+    odd = np.count_nonzero((np.abs(ref) < 127) & (np.abs(ref) > 0))
+    assert odd > 1000
+    assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatches"
+    wt.release()
+
+
 @pytest.mark.parametrize("layout", [0, 1])
 def test_i8_conv_groups_dilation_zero_point(ctx, layout):
     r = rng(31)
