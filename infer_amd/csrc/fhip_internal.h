@@ -34,6 +34,7 @@ struct fhip_weight_s;
 
 struct fhip_context_s {
     int device = 0;
+    int cus = 256;  // compute units of the device (grid sizing)
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     size_t workspace_limit = SIZE_MAX;

@@ -225,6 +225,9 @@ int fhip_context_create(int device, fhip_context* out) {
     DeviceGuard guard(device);
     auto* ctx = new fhip_context_s();
     ctx->device = device;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
+        ctx->cus = cus;
     if (hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess) {
         delete ctx;
         return FHIP_ERR_HIP;

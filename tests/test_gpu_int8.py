@@ -198,6 +198,26 @@ def test_i8_conv_config4_bitexact(ctx, pow2):
     wt.release()
 
 
+def test_i8_conv_window_128_channel_blocks(ctx):
+    """A grid large enough (here 1024 blocks) for the window kernel's 128-output-channel blocks, with OC
+    = 160 ending in a partial block; smaller grids (C4 among them) take 64-channel blocks."""
+    r = rng(53)
+    n, c, h, wd, oc = 4, 64, 64, 64, 160
+    x = r.integers(-128, 128, (n, c, h, wd)).astype(np.int8)
+    w = r.integers(-127, 128, (oc, c, 3, 3)).astype(np.int8)
+    s_w = r.uniform(1e-3, 1e-2, oc).astype(np.float32)
+    bias = r.integers(-3000, 3000, oc).astype(np.int32)
+    rc, ref = po.i8_conv2d(x, 0.03, 3, w, s_w, bias, 1, 1, 0.4, -2)
+    assert rc == 0
+    wt = ctx.prepare_conv_weight(dev(w), s_w, version=8)
+    out = torch.empty(ref.shape, dtype=torch.int8, device="cuda")
+    ctx.i8_conv2d(dev(x), 0, 0.03, 3, wt, out, 0.4, -2, stride=(1, 1), pad=(1, 1), bias=dev(bias), bias_abs_max=3000)
+    assert ctx.last_backend() == "i8_mfma_conv_window"
+    got = out.cpu().numpy()
+    assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatches"
+    wt.release()
+
+
 @pytest.mark.parametrize("sign", [1, -1])
 def test_i8_conv_requant_near_ties(ctx, sign):
     """The conv epilogue's requantization on values just off an x.5 point: with s_in * s_w / s_out =
