@@ -563,6 +563,11 @@ class HipQwenGemmArgmaxKernel final : public KernelBase {
         if (p->a->data_type() != dtype || p->b->data_type() != dtype || p->b->dims().size() != 2)
             return Unsupported("QwenGemmArgmax operand dtypes");
         if (IsFp8(dtype) && (!PerTensor(*p->a) || !PerTensor(*p->b))) return Unsupported("per-tensor FP8 scales only");
+        // the library's row limits (include/fhip.h): rows of whole 16-byte chunks, at most 64 KiB, V < 2^32
+        const int64_t k = p->b->dims()[1], v = p->b->dims()[0];
+        const int64_t row_bytes = k * (dtype == DataType::BF16 ? 2 : 1);
+        if (row_bytes % 16 != 0 || row_bytes > 65536 || v >= (int64_t(1) << 32))
+            return Unsupported("QwenGemmArgmax row length or vocabulary beyond the HIP kernel's limits");
         return Status::Ok();
     }
     int32_t compute() override {
