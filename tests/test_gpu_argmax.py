@@ -140,6 +140,23 @@ def test_bf16_argmax_row_lengths(ctx, m, k):
         assert np.max(np.abs(lg[j] - ref)) <= 1e-2 * np.max(np.abs(ref))
 
 
+@pytest.mark.parametrize("m,k,v", [(1, 8, 1), (1, 8, 5), (1, 24, 33), (1, 520, 7), (1, 1032, 3), (3, 8, 2),
+                                   (2, 4104, 9)])
+def test_bf16_argmax_tiny_and_ragged_heads(ctx, m, k, v):
+    """Heads smaller than one row group of one wave (V = 1, 2, 5), rows shorter than a segment (K = 8: 16
+    bytes; 24), rows ending inside a segment (K = 520, 1032, 4104), and an MFMA-kernel head with fewer rows
+    than one tile: every lane and row past the end must contribute nothing."""
+    a, w = head_inputs(SEEDS[5] + 1000 + 31 * k + v, m, k, v)
+    tokens = torch.empty(m, dtype=torch.int64, device="cuda")
+    logits = torch.empty((m, v), dtype=torch.float32, device="cuda")
+    ctx.bf16_gemv_argmax(dev(a), dev(w), tokens, logits)
+    assert check_tokens(a, w, tokens.cpu().numpy()) == 0
+    lg = logits.cpu().numpy()
+    for j in range(m):
+        _, ref = po.bf16_gemm_argmax(a[j], w, want_logits=True)
+        assert np.max(np.abs(lg[j] - ref)) <= 1e-2 * max(np.max(np.abs(ref)), 1e-30)
+
+
 def test_bf16_argmax_rejects_longer_rows(ctx):
     """Rows beyond 64 KiB (K > 32768 BF16) are refused with FHIP_ERR_UNSUPPORTED, not computed wrongly."""
     from infer_amd.runtime import FhipError
@@ -162,10 +179,10 @@ def test_bf16_argmax_repeated_calls_rearm(ctx):
 
 
 @pytest.mark.parametrize("dtype", [po.FP8E4M3, po.FP8E5M2])
-@pytest.mark.parametrize("m,k", [(1, 1024), (5, 1024), (3, 4096), (1, 512), (1, 6144), (2, 8192)])
-def test_fp8_argmax_head(ctx, dtype, m, k):
+@pytest.mark.parametrize("m,k,v", [(1, 1024, 32768), (5, 1024, 32768), (3, 4096, 32768), (1, 512, 32768),
+                                   (1, 6144, 32768), (2, 8192, 32768), (1, 16, 7), (2, 48, 3), (1, 1040, 5)])
+def test_fp8_argmax_head(ctx, dtype, m, k, v):
     from tests.common import fp8_tensor, fp8_pow2_scale
-    v = 32768
     r = rng(SEEDS[5] + m)
     a_codes, sa = fp8_tensor(r.standard_normal((m, k)).astype(np.float32), dtype)
     w_codes, sw = fp8_tensor(r.standard_normal((v, k), dtype=np.float32) * np.float32(0.02), dtype)
