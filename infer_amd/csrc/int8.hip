@@ -330,7 +330,10 @@ constexpr int kWinSpan = kWinCols / 4 + 1;
 constexpr int kWinChunks = 5;
 __host__ __device__ constexpr int conv_chunks(int wx) { return (wx + 15 + 15) / 16; }
 
-template <int WNF, int TAPS>
+// STG = 1: compiled for the 16-byte NCHW staging path only (the host checks its conditions).  A launch
+// is latency-bound and starts with a cold instruction cache, so code the shape never runs still costs:
+// on C4 the 16-byte-only kernel spans 5.1 us in-kernel against 5.6 us for the general one.
+template <int WNF, int TAPS, int STG = 0>
 __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __restrict__ in, ConvGeom g,
                                                              const int8_t* __restrict__ wt,
                                                              const int32_t* __restrict__ bias, I8Epilogue ep,
@@ -340,7 +343,8 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int64_t ox0 = (int64_t)blockIdx.x * kConvTox;
-    const int64_t b = blockIdx.y / g.oh, oy = blockIdx.y % g.oh;
+    // 32-bit: the grid's y extent is n * oh < 2^31 (a 64-bit division is a long scalar sequence)
+    const int64_t b = (int)blockIdx.y / (int)g.oh, oy = (int)blockIdx.y % (int)g.oh;
     const int64_t oc_base = (int64_t)blockIdx.z * (4 * WNF * 16) + wave * (WNF * 16);
     const int wx = (kConvTox - 1) * g.sw + (int)((g.kw - 1) * g.dw) + 1;
     const int64_t taps = g.kh * g.kw;
@@ -375,14 +379,15 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
     const uint8_t zp = (uint8_t)g.zp_in;
     // NCHW 16-byte path: rows a multiple of 16 bytes, 16-byte aligned input, kh * 16 * chunks threads.
     const int chunks = conv_chunks(wx);
-    const bool vec_rows = g.layout == FHIP_NCHW && (g.w & 15) == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0 &&
-                          chunks <= kWinChunks && g.kh * 16 * chunks <= 256;
+    const bool vec_rows = STG == 1 || (g.layout == FHIP_NCHW && (g.w & 15) == 0 &&
+                                       (reinterpret_cast<uintptr_t>(in) & 15) == 0 && chunks <= kWinChunks &&
+                                       g.kh * 16 * chunks <= 256);
     // window row length in LDS and the column of the first window byte in it
     const int wrow = vec_rows ? 16 * chunks : wx;
     const int a0 = ix0 >= 0 ? ix0 & ~15 : -((-ix0 + 15) & ~15);  // floor to a multiple of 16
     const int xsh = vec_rows ? ix0 - a0 : 0;
     // NCHW dword path: rows 4-byte aligned, at most 4 tap rows, a window of at most 80 columns.
-    const bool dword_rows = !vec_rows && g.layout == FHIP_NCHW && (g.w & 3) == 0 &&
+    const bool dword_rows = STG != 1 && !vec_rows && g.layout == FHIP_NCHW && (g.w & 3) == 0 &&
                             (reinterpret_cast<uintptr_t>(in) & 3) == 0 && wx <= 4 * kWinCols && g.kh * 64 <= 256;
     for (int64_t c0 = 0; c0 < g.c; c0 += 64) {
         // 1. issue this thread's window loads (fast path), then every tap's weight fragments; nothing
@@ -562,8 +567,17 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
                     acc[f][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[f], bf[j], acc[f][j], 0, 0, 0);
         };
         if constexpr (TAPS > 0) {
+            // tap t = ky * kw + kx, stepped incrementally (kw is a kernel argument: no division per tap)
+            int ky = 0, kx = 0;
+            const int kw = (int)g.kw;
 #pragma unroll
-            for (int t = 0; t < TAPS; ++t) tap_step(t / g.kw, t % g.kw, bpre[t]);
+            for (int t = 0; t < TAPS; ++t) {
+                tap_step(ky, kx, bpre[t]);
+                if (++kx == kw) {
+                    kx = 0;
+                    ++ky;
+                }
+            }
         } else {
             for (int64_t ky = 0; ky < g.kh; ++ky)
                 for (int64_t kx = 0; kx < g.kw; ++kx) {
@@ -591,7 +605,7 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
             const uint32_t packed = (uint32_t)(uint8_t)q[0] | ((uint32_t)(uint8_t)q[1] << 8) |
                                     ((uint32_t)(uint8_t)q[2] << 16) | ((uint32_t)(uint8_t)q[3] << 24);
             const int64_t ox = ox0 + f * 16 + (lane >> 4) * 4;
-            if (g.layout == FHIP_NCHW) {
+            if (STG == 1 || g.layout == FHIP_NCHW) {
                 int8_t* dst = ep.out + ((b * oc_total + oc) * g.oh + oy) * g.ow + ox;
                 if (ox + 3 < g.ow && ((reinterpret_cast<uintptr_t>(dst) & 3) == 0)) {
                     *reinterpret_cast<uint32_t*>(dst) = packed;
@@ -799,7 +813,14 @@ int fhip_i8_conv2d(fhip_context ctx, const int8_t* in, int64_t n, int64_t c, int
                       (unsigned)((oc + 4 * wnf * 16 - 1) / (4 * wnf * 16)));
             const int8_t* tm = static_cast<const int8_t*>(wt->tap_major);
             const bool t9 = wt->kh * wt->kw == 9;
-            if (wnf == 2 && t9) i8_conv_window_kernel<2, 9><<<grid, 256, lds, ctx->stream>>>(in, g, tm, bias, ep, oc);
+            // the kernel's 16-byte staging conditions (vec_rows), decided here to pick the specialized build
+            const bool vec = layout == FHIP_NCHW && (w & 15) == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0 &&
+                             conv_chunks(wx) <= kWinChunks && wt->kh * 16 * conv_chunks(wx) <= 256;
+            if (vec && wnf == 2 && t9) i8_conv_window_kernel<2, 9, 1><<<grid, 256, lds, ctx->stream>>>(in, g, tm, bias, ep, oc);
+            else if (vec && wnf == 2) i8_conv_window_kernel<2, 0, 1><<<grid, 256, lds, ctx->stream>>>(in, g, tm, bias, ep, oc);
+            else if (vec && t9) i8_conv_window_kernel<1, 9, 1><<<grid, 256, lds, ctx->stream>>>(in, g, tm, bias, ep, oc);
+            else if (vec) i8_conv_window_kernel<1, 0, 1><<<grid, 256, lds, ctx->stream>>>(in, g, tm, bias, ep, oc);
+            else if (wnf == 2 && t9) i8_conv_window_kernel<2, 9><<<grid, 256, lds, ctx->stream>>>(in, g, tm, bias, ep, oc);
             else if (wnf == 2) i8_conv_window_kernel<2, 0><<<grid, 256, lds, ctx->stream>>>(in, g, tm, bias, ep, oc);
             else if (t9) i8_conv_window_kernel<1, 9><<<grid, 256, lds, ctx->stream>>>(in, g, tm, bias, ep, oc);
             else i8_conv_window_kernel<1, 0><<<grid, 256, lds, ctx->stream>>>(in, g, tm, bias, ep, oc);
