@@ -649,6 +649,18 @@ __global__ void quantize_kernel(const void* __restrict__ src, int src_dtype, int
     }
 }
 
+// Per-tensor QuantizeLinear (one scale, one zero point; the C1 activation): the source type is a template
+// parameter and the division x / s becomes requant_i8's multiply by 1/s with the exact division near an x.5
+// point, which yields the same clamp(round_away(double(x) / double(s) + zp)) -- also for NaN and Inf, whose
+// t is NaN and so takes the division.  No per-channel index arithmetic is compiled in.
+template <int SRC>
+__global__ void quantize_tensor_kernel(const void* __restrict__ src, int64_t count, float scale, int32_t zp,
+                                       int8_t* __restrict__ out) {
+    const double s = scale, r = 1.0 / s, z = zp;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = requant_i8((double)read_float(src, SRC, i), s, r, z);
+}
+
 __global__ void dequantize_kernel(const int8_t* __restrict__ src, int64_t count, int64_t channels, int64_t inner,
                                   QParams inline_params, const float* __restrict__ scales,
                                   const int32_t* __restrict__ zps, int per_channel_zp, int dst_dtype, void* out) {
@@ -852,8 +864,19 @@ int fhip_quantize_linear(fhip_context ctx, int src_dtype, const void* src, int64
     const float* ds;
     const int32_t* dz;
     if ((rc = upload_params(ctx, channels, scales, zero_points, n_zp, &qp, &ds, &dz)) != FHIP_OK) return rc;
-    quantize_kernel<<<grid_for(count, 256), 256, 0, ctx->stream>>>(src, src_dtype, count, channels, inner, qp, ds, dz,
-                                                                    n_zp > 1 ? 1 : 0, out);
+    if (channels == 1 && !ds) {  // per tensor, parameters inline
+        const float sc = qp.scale[0];
+        const int32_t z = qp.zp[0];
+        if (src_dtype == FHIP_FP32)
+            quantize_tensor_kernel<FHIP_FP32><<<grid_for(count, 256), 256, 0, ctx->stream>>>(src, count, sc, z, out);
+        else if (src_dtype == FHIP_BF16)
+            quantize_tensor_kernel<FHIP_BF16><<<grid_for(count, 256), 256, 0, ctx->stream>>>(src, count, sc, z, out);
+        else
+            quantize_tensor_kernel<FHIP_FP16><<<grid_for(count, 256), 256, 0, ctx->stream>>>(src, count, sc, z, out);
+    } else {
+        quantize_kernel<<<grid_for(count, 256), 256, 0, ctx->stream>>>(src, src_dtype, count, channels, inner, qp, ds,
+                                                                        dz, n_zp > 1 ? 1 : 0, out);
+    }
     ctx->last_backend = "quantize_linear";
     FHIP_CHECK_LAUNCH(ctx, "quantize_kernel");
     return FHIP_OK;

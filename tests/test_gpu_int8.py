@@ -46,6 +46,20 @@ def test_quantize_linear_fp32_per_tensor(ctx):
 
 
 @pytest.mark.parametrize("src_dtype", [po.BF16, po.FP16])
+def test_quantize_linear_half_per_tensor_every_code(ctx, src_dtype):
+    """Per-tensor QuantizeLinear (the reciprocal-multiply kernel) over all 65536 BF16 / FP16 codes: NaN, Inf,
+    subnormals, and, at power-of-two scales, exact x.5 ties that must go to the division and round away."""
+    codes = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    for scale, zp in ((0.25, 0), (2.0 ** -7, 3), (0.0123, -5), (3.0, 127)):
+        out = torch.empty(codes.shape, dtype=torch.int8, device="cuda")
+        ctx.quantize_linear(dev(codes), src_dtype, [scale], [zp], out)
+        rc, ref = po.quantize_linear(src_dtype, codes, [scale], [zp])
+        assert rc == 0
+        got = out.cpu().numpy()
+        assert np.array_equal(got, ref), f"scale {scale} zp {zp}: {np.count_nonzero(got != ref)} mismatches"
+
+
+@pytest.mark.parametrize("src_dtype", [po.BF16, po.FP16])
 def test_quantize_linear_half_per_channel(ctx, src_dtype):
     r = rng(5)
     x = r.standard_normal((4, 200, 3)).astype(np.float32)
