@@ -200,7 +200,10 @@ __global__ __launch_bounds__(kGemvThreads) void fp8_gemv_mfma_kernel(const void*
 // re-encodes the batch with the reference's saturated / special codes (encode4) in one cold branch.
 // NW waves split K (wave w takes the steps w, w + NW, ...), U steps per load batch; the NW partial 16x16
 // tiles are summed through LDS.
-template <bool E5, int ADT, int U, bool POW2, int NW>
+// OB: 0 = the general epilogue (ep.store); 1, 2, 4 = output bytes (FP8 code, BF16, FP32) for a power-of-two
+// output scale, with the M = 1 kernel's hardware-converter encode -- a short, branch-free tail in place of
+// the general one's software codec and division (the tail runs once per launch with a cold instruction cache).
+template <bool E5, int ADT, int U, bool POW2, int NW, int OB = 0>
 __global__ __launch_bounds__(NW * 64) void fp8_gemv_mfma_reg_kernel(const void* __restrict__ a, float a_scale,
                                                                           float a_inv, int64_t m, int64_t k,
                                                                           const uint8_t* __restrict__ w, int64_t kp,
@@ -307,7 +310,24 @@ __global__ __launch_bounds__(NW * 64) void fp8_gemv_mfma_reg_kernel(const void* 
         float sum = red[0][row][cc];
 #pragma unroll
         for (int q = 1; q < NW; ++q) sum += red[q][row][cc];
-        if (row < m && col < n) ep.store(sum, row, col);
+        if (row < m && col < n) {
+            if constexpr (OB == 0) {
+                ep.store(sum, row, col);
+            } else {
+                // the general epilogue's order: acc*ab_scale, *alpha, [+ beta*bias], then * (1/out_scale)
+                float y = sum * ep.ab_scale;
+                y *= ep.alpha;
+                if (ep.bias_kind != FHIP_BIAS_NONE) {
+                    const uint8_t bc = ep.bias[ep.bias_kind == FHIP_BIAS_VECTOR ? col : row * ep.n + col];
+                    y += ep.beta * (fhip::fp8_decode(bc, E5) * ep.bias_scale);
+                }
+                const uint32_t code = encode1<E5>(y * ep.out_inv);
+                const int64_t idx = row * ep.n + col;
+                if constexpr (OB == 1) static_cast<uint8_t*>(ep.out)[idx] = (uint8_t)code;
+                else if constexpr (OB == 2) static_cast<uint16_t*>(ep.out)[idx] = fhip::bf16_encode(decode_code<E5>(code) * ep.out_scale);
+                else static_cast<float*>(ep.out)[idx] = decode_code<E5>(code) * ep.out_scale;
+            }
+        }
     }
 }
 
@@ -588,17 +608,27 @@ int launch_gemv_t(fhip_context ctx, const void* a, float a_scale, int64_t m, con
         const unsigned grid = (unsigned)((w->n + 15) / 16);
         // 8 waves split K (one 128-deep step each per batch at K <= 1024), so each lane encodes 32 activations
         // per step of its own and two waves per SIMD cover each other's encode latency
-#define FHIP_REG_LAUNCH(U, P2)                                                                                    \
-    fp8_gemv_mfma_reg_kernel<E5, ADT, U, P2, 8><<<grid, 8 * 64, 0, ctx->stream>>>(a, a_scale, a_inv, m, w->k, wd, kp, \
-                                                                                  w->n, ep)
+#define FHIP_REG_LAUNCH(U, P2, OB)                                                                                \
+    fp8_gemv_mfma_reg_kernel<E5, ADT, U, P2, 8, OB><<<grid, 8 * 64, 0, ctx->stream>>>(a, a_scale, a_inv, m, w->k, wd, \
+                                                                                      kp, w->n, ep)
+#define FHIP_REG_LAUNCH_OB(U)                                                                                     \
+    do {                                                                                                          \
+        if (ob == 1) FHIP_REG_LAUNCH(U, true, 1);                                                                 \
+        else if (ob == 2) FHIP_REG_LAUNCH(U, true, 2);                                                            \
+        else if (ob == 4) FHIP_REG_LAUNCH(U, true, 4);                                                            \
+        else FHIP_REG_LAUNCH(U, true, 0);                                                                         \
+    } while (0)
         const bool p2 = a_inv != 0.0f;
+        // power-of-two activation and output scales (decode): the specialized output tail
+        const int ob = ep.out_inv == 0.0f ? 0 : (ep.out_dtype == FHIP_BF16 ? 2 : (ep.out_dtype == FHIP_FP32 ? 4 : 1));
         if (kp / 128 <= 8) {
-            if (p2) FHIP_REG_LAUNCH(1, true);
-            else FHIP_REG_LAUNCH(1, false);
+            if (p2) FHIP_REG_LAUNCH_OB(1);
+            else FHIP_REG_LAUNCH(1, false, 0);
         } else {
-            if (p2) FHIP_REG_LAUNCH(2, true);
-            else FHIP_REG_LAUNCH(2, false);
+            if (p2) FHIP_REG_LAUNCH_OB(2);
+            else FHIP_REG_LAUNCH(2, false, 0);
         }
+#undef FHIP_REG_LAUNCH_OB
 #undef FHIP_REG_LAUNCH
         ctx->last_backend = "fp8_gemv_mfma";
         FHIP_CHECK_LAUNCH(ctx, "fp8_gemv_mfma_reg_kernel");

@@ -246,6 +246,33 @@ def test_fp8_gemm_bias_alpha_beta(ctx):
     wt.release()
 
 
+@pytest.mark.parametrize("out_dtype", [po.FP32, po.BF16])
+def test_fp8_gemv_bias_alpha_beta_decoded_outputs(ctx, out_dtype):
+    """Decode GEMV (m = 4 and 16, the register kernel's specialized output tail for power-of-two output
+    scales) with a vector bias, alpha and beta, writing decoded FP32 / BF16: the values re-encode to codes
+    within one of the oracle's, and decode exactly."""
+    dtype = po.FP8E4M3
+    k, n = 256, 96
+    a, sa, w_nk, w_src, sw, s_out = _linear_case(13, dtype, 16, k, n, 1)
+    bias_f = rng(14).standard_normal(n).astype(np.float32) * 0.1
+    bias, sb = fp8_tensor(bias_f, dtype)
+    wt = ctx.prepare_weight(dev(w_src), dtype, k, n, 1, version=5)
+    for mm in (4, 16):
+        esz = 4 if out_dtype == po.FP32 else 2
+        out = torch.empty((mm, n * esz), dtype=torch.uint8, device="cuda")
+        ctx.fp8_linear(dev(a[:mm]), dtype, sa, mm, wt, sw, out, out_dtype, s_out, bias=dev(bias), bias_scale=sb,
+                       bias_kind=po.BIAS_VECTOR, alpha=0.5, beta=2.0)
+        assert ctx.last_backend() == "fp8_gemv_mfma"
+        ref = po.fp8_gemm(dtype, a[:mm], sa, w_nk, sw, True, s_out, bias=bias, s_bias=sb, bias_kind=po.BIAS_VECTOR,
+                          alpha=0.5, beta=2.0)
+        raw = host(out).reshape(mm, n * esz)
+        got = raw.view(np.float32) if out_dtype == po.FP32 else raw.view(np.uint16)
+        codes = po.cast_to_fp8(out_dtype, got, dtype, s_out)
+        assert np.array_equal(po.cast_from_fp8(dtype, codes, s_out, out_dtype), got)
+        assert fp8_code_distance(codes, ref).max() <= 1
+    wt.release()
+
+
 def test_fp8_gemm_bias_alpha_beta_full_size(ctx):
     """Bias, alpha and beta on the up-projection shape (256x224 tiles, power-of-two output scale with a
     bias: the unfolded epilogue); a seeded subset of rows against the oracle."""
