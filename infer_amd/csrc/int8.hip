@@ -38,11 +38,17 @@ __device__ __forceinline__ int8_t clamp_round_i8(double t) {
 // form by at most ~2^-51 * (|t| + |zp_out|) (the reciprocal and the product are each correctly rounded);
 // round() changes value only at the x.5 points, so wherever t is farther than that from one both forms
 // round to the same integer.  Only near an x.5 point (or for non-finite t) is the division done.
-__device__ __forceinline__ int8_t requant_i8(double real, double s_out, double recip_out, double zp_out) {
+__device__ __forceinline__ int8_t requant_i8_fast(double real, double recip_out, double zp_out, bool& near_tie) {
     const double t = real * recip_out + zp_out;
     const double half_gap = fabs((t - floor(t)) - 0.5);
-    if (!(half_gap > 0x1p-40 * (fabs(t) + 256.0))) return clamp_round_i8(real / s_out + zp_out);
+    near_tie = !(half_gap > 0x1p-40 * (fabs(t) + 256.0));
     return clamp_round_i8(t);
+}
+__device__ __forceinline__ int8_t requant_i8(double real, double s_out, double recip_out, double zp_out) {
+    bool near_tie;
+    const int8_t q = requant_i8_fast(real, recip_out, zp_out, near_tie);
+    if (near_tie) return clamp_round_i8(real / s_out + zp_out);
+    return q;
 }
 
 struct I8Epilogue {
@@ -588,20 +594,43 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
         }
     }
     // C fragment of lane l: channel l%16, pixels 4*(l/16) .. +3 (consecutive output x).
+    // Requantize every value on the reciprocal path first; values near an x.5 point are redone with the
+    // division in one cold branch (rare), so the hot tail holds no per-value branch.
+    int8_t qv[kConvFrags][WNF][4];
+    uint32_t ties = 0;
+#pragma unroll
+    for (int f = 0; f < kConvFrags; ++f)
+#pragma unroll
+        for (int j = 0; j < WNF; ++j) {
+            const double scale = (double)ep.s_a * (double)e_scale[j];
+            const int32_t shift = e_bias[j] - (int32_t)g.zp_in * e_wsum[j];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                bool tie;
+                qv[f][j][r] = requant_i8_fast((double)(acc[f][j][r] + shift) * scale, ep.recip_out, ep.zp_out, tie);
+                ties |= (uint32_t)tie << ((f * WNF + j) * 4 + r);
+            }
+        }
+    if (__builtin_expect(ties != 0, 0)) {
+#pragma unroll
+        for (int f = 0; f < kConvFrags; ++f)
+#pragma unroll
+            for (int j = 0; j < WNF; ++j) {
+                const double scale = (double)ep.s_a * (double)e_scale[j];
+                const int32_t shift = e_bias[j] - (int32_t)g.zp_in * e_wsum[j];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if ((ties >> ((f * WNF + j) * 4 + r)) & 1u)
+                        qv[f][j][r] = clamp_round_i8((double)(acc[f][j][r] + shift) * scale / ep.inv_out_den + ep.zp_out);
+            }
+    }
 #pragma unroll
     for (int f = 0; f < kConvFrags; ++f)
 #pragma unroll
         for (int j = 0; j < WNF; ++j) {
             const int64_t oc = oc_base + j * 16 + (lane & 15);
             if (oc >= oc_total) continue;
-            const double scale = (double)ep.s_a * (double)e_scale[j];
-            const int32_t shift = e_bias[j] - (int32_t)g.zp_in * e_wsum[j];
-            int8_t q[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const double real = (double)(acc[f][j][r] + shift) * scale;
-                q[r] = requant_i8(real, ep.inv_out_den, ep.recip_out, ep.zp_out);
-            }
+            const int8_t (&q)[4] = qv[f][j];
             const uint32_t packed = (uint32_t)(uint8_t)q[0] | ((uint32_t)(uint8_t)q[1] << 8) |
                                     ((uint32_t)(uint8_t)q[2] << 16) | ((uint32_t)(uint8_t)q[3] << 24);
             const int64_t ox = ox0 + f * 16 + (lane >> 4) * 4;
