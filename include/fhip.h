@@ -104,7 +104,7 @@ int fhip_memory_copy(fhip_context ctx, void* dst, const void* src, size_t bytes)
 int fhip_weight_prepare(fhip_context ctx, const void* src, int dtype, int64_t k, int64_t n, int src_layout,
                         const float* scales, int64_t n_scale, const int32_t* zero_points, int64_t n_zp,
                         uint64_t version, fhip_weight* out);
-/* The same preparation from host memory, at model load (SURVEY's load-time pre-swizzle): the bytes are
+/* The same preparation from host memory, at model load (a load-time pre-swizzle): the bytes are
  * uploaded, re-laid out as above and keyed on (host_src, dtype, K, N, layout, version), so a loader can
  * prepare every immutable weight once straight from the (mmapped) model file instead of at the first
  * Prepare() from a device tensor (src/model/model_io.cc, weight_store.cc; kernel.h:160-162).  The
