@@ -209,42 +209,57 @@ struct ConvGeom {
     int8_t zp_in;
 };
 
-__device__ __forceinline__ void conv_gather16(const int8_t* __restrict__ in, const ConvGeom& g, int64_t pix, int group,
-                                              int64_t kk0, uint32_t* out4) {
+// One output pixel's input geometry, computed once per lane and fragment row (the host keeps n*oh*ow, h*w and
+// the padded K below 2^31, so the splits are 32-bit).
+struct ConvPix {
+    bool live;
+    int iy0, ix0;   // input coordinates of tap (0, 0)
+    int64_t base;   // element offset of (b, first channel of the group, 0, 0)
+};
+
+__device__ __forceinline__ ConvPix conv_pix(const ConvGeom& g, int64_t pix, int group) {
+    ConvPix p{false, 0, 0, 0};
+    const int ohw = (int)(g.oh * g.ow);
+    if (pix >= (int64_t)g.n * ohw) return p;
+    const int q = (int)pix;
+    const int b = q / ohw, rem = q - b * ohw;
+    const int oy = rem / (int)g.ow, ox = rem - oy * (int)g.ow;
+    p.live = true;
+    p.iy0 = oy * g.sh - g.ph;
+    p.ix0 = ox * g.sw - g.pw;
+    const int64_t c0 = (int64_t)group * g.icg;
+    p.base = g.layout == FHIP_NCHW ? ((int64_t)b * g.c + c0) * g.h * g.w : (int64_t)b * g.h * g.w * g.c + c0;
+    return p;
+}
+
+// 16 consecutive K elements (weight order ci, ky, kx) of one pixel's implicit-GEMM row, from kk0.
+__device__ __forceinline__ void conv_gather16(const int8_t* __restrict__ in, const ConvGeom& g, const ConvPix& p,
+                                              int kk0, uint32_t* out4) {
     uint8_t bytes[16];
-    const int64_t np = g.n * g.oh * g.ow;
-    if (pix >= np) {
+    const int kw = (int)g.kw, kh = (int)g.kh, khw = kh * kw, w = (int)g.w, h = (int)g.h, k = (int)g.k;
+    int ci = kk0 / khw;
+    const int r2 = kk0 - ci * khw;
+    int ky = r2 / kw, kx = r2 - ky * kw;
+    const int64_t plane = (int64_t)h * w;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) bytes[i] = 0;
-    } else {
-        const int64_t b = pix / (g.oh * g.ow);
-        const int64_t rem = pix - b * g.oh * g.ow;
-        const int64_t oy = rem / g.ow, ox = rem - (rem / g.ow) * g.ow;
-        const int64_t khw = g.kh * g.kw;
-        int64_t ci = kk0 / khw;
-        int64_t r2 = kk0 - ci * khw;
-        int64_t ky = r2 / g.kw, kx = r2 - (r2 / g.kw) * g.kw;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            uint8_t v = 0;
-            if (kk0 + i < g.k) {
-                const int64_t iy = oy * g.sh - g.ph + ky * g.dh;
-                const int64_t ix = ox * g.sw - g.pw + kx * g.dw;
-                v = (uint8_t)g.zp_in;
-                if (iy >= 0 && iy < g.h && ix >= 0 && ix < g.w) {
-                    const int64_t cc = group * g.icg + ci;
-                    const int64_t off = g.layout == FHIP_NCHW ? ((b * g.c + cc) * g.h + iy) * g.w + ix
-                                                              : ((b * g.h + iy) * g.w + ix) * g.c + cc;
-                    v = (uint8_t)in[off];
-                }
+    for (int i = 0; i < 16; ++i) {
+        uint8_t v = 0;
+        if (p.live && kk0 + i < k) {
+            const int iy = p.iy0 + ky * (int)g.dh;
+            const int ix = p.ix0 + kx * (int)g.dw;
+            v = (uint8_t)g.zp_in;
+            if (iy >= 0 && iy < h && ix >= 0 && ix < w) {
+                const int64_t off = g.layout == FHIP_NCHW ? p.base + ci * plane + (int64_t)(iy * w + ix)
+                                                          : p.base + (int64_t)(iy * w + ix) * g.c + ci;
+                v = (uint8_t)in[off];
             }
-            bytes[i] = v;
-            if (++kx == g.kw) {
-                kx = 0;
-                if (++ky == g.kh) {
-                    ky = 0;
-                    ++ci;
-                }
+        }
+        bytes[i] = v;
+        if (++kx == kw) {
+            kx = 0;
+            if (++ky == kh) {
+                ky = 0;
+                ++ci;
             }
         }
     }
@@ -271,12 +286,15 @@ __global__ __launch_bounds__(256) void i8_conv_kernel(const int8_t* __restrict__
     for (int i = 0; i < WM; ++i)
 #pragma unroll
         for (int j = 0; j < WN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
-    for (int64_t k0 = 0; k0 < g.k; k0 += 64) {
+    ConvPix px[WM];
+#pragma unroll
+    for (int i = 0; i < WM; ++i) px[i] = conv_pix(g, pix_base + i * 16 + fr, group);
+    for (int k0 = 0; k0 < (int)g.k; k0 += 64) {
         v4i af[WM], bf[WN];
 #pragma unroll
         for (int i = 0; i < WM; ++i) {
             uint32_t v[4];
-            conv_gather16(in, g, pix_base + i * 16 + fr, group, k0 + fk, v);
+            conv_gather16(in, g, px[i], k0 + fk, v);
             af[i] = v4i{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
         }
 #pragma unroll
@@ -302,9 +320,10 @@ __global__ __launch_bounds__(256) void i8_conv_kernel(const int8_t* __restrict__
             for (int r = 0; r < 4; ++r) {
                 const int64_t pix = pix_base + i * 16 + (lane >> 4) * 4 + r;
                 if (pix >= np) continue;
-                const int64_t b = pix / (g.oh * g.ow);
-                const int64_t rem = pix - b * g.oh * g.ow;
-                const int64_t oy = rem / g.ow, ox = rem - oy * g.ow;
+                const int ohw = (int)(g.oh * g.ow), q = (int)pix;  // np < 2^31 (host-checked)
+                const int64_t b = q / ohw;
+                const int rem = q - (int)b * ohw;
+                const int64_t oy = rem / (int)g.ow, ox = rem - (int)oy * (int)g.ow;
                 const int32_t dot = acc[i][j][r] - (int32_t)g.zp_in * ep.wsum[oc];
                 const int32_t total = dot + (bias ? bias[oc] : 0);
                 const double real = (double)total * ((double)ep.s_a * (double)ep.w_scales[oc]);
@@ -872,6 +891,8 @@ int fhip_i8_conv2d(fhip_context ctx, const int8_t* in, int64_t n, int64_t c, int
     }
     constexpr int WM = 2, WN = 2;
     const int64_t np = n * oh * ow;
+    if (np >= (int64_t(1) << 31) || h * w >= (int64_t(1) << 31) || (np + 32 * WM - 1) / (32 * WM) > 65535)
+        return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "i8_conv2d: image too large for the gathered conv kernel");
     dim3 grid((unsigned)((g.ocg + 32 * WN - 1) / (32 * WN)), (unsigned)((np + 32 * WM - 1) / (32 * WM)),
               (unsigned)wt->group);
     i8_conv_kernel<WM, WN><<<grid, 256, 0, ctx->stream>>>(in, g, static_cast<const int8_t*>(wt->data), bias, ep);
