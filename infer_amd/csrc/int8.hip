@@ -277,61 +277,116 @@ __global__ __launch_bounds__(256) void i8_conv_kernel(const int8_t* __restrict__
     const int wave = threadIdx.x >> 6;
     const int group = blockIdx.z;
     const int64_t np = g.n * g.oh * g.ow;
-    const int64_t pix_base = (int64_t)blockIdx.y * (32 * WM) + (wave >> 1) * (16 * WM);
     const int64_t oc_base = (int64_t)blockIdx.x * (32 * WN) + (wave & 1) * (16 * WN);  // within the group
     const int fr = lane & 15;
     const int fk = (lane >> 4) * 16;
-    v4i acc[WM][WN];
+    // pixel tiles of 32*WM rows, grid-strided over y (the grid's y extent is capped at 65535)
+    const int64_t tiles_y = (np + 32 * WM - 1) / (32 * WM);
+    for (int64_t ty = blockIdx.y; ty < tiles_y; ty += gridDim.y) {
+        const int64_t pix_base = ty * (32 * WM) + (wave >> 1) * (16 * WM);
+        v4i acc[WM][WN];
 #pragma unroll
-    for (int i = 0; i < WM; ++i)
+        for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int j = 0; j < WN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
-    ConvPix px[WM];
+            for (int j = 0; j < WN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+        ConvPix px[WM];
 #pragma unroll
-    for (int i = 0; i < WM; ++i) px[i] = conv_pix(g, pix_base + i * 16 + fr, group);
-    for (int k0 = 0; k0 < (int)g.k; k0 += 64) {
-        v4i af[WM], bf[WN];
+        for (int i = 0; i < WM; ++i) px[i] = conv_pix(g, pix_base + i * 16 + fr, group);
+        for (int k0 = 0; k0 < (int)g.k; k0 += 64) {
+            v4i af[WM], bf[WN];
 #pragma unroll
-        for (int i = 0; i < WM; ++i) {
-            uint32_t v[4];
-            conv_gather16(in, g, px[i], k0 + fk, v);
-            af[i] = v4i{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
-        }
+            for (int i = 0; i < WM; ++i) {
+                uint32_t v[4];
+                conv_gather16(in, g, px[i], k0 + fk, v);
+                af[i] = v4i{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
+            }
 #pragma unroll
-        for (int j = 0; j < WN; ++j) {
-            int64_t oc = oc_base + j * 16 + fr;
-            oc = oc < g.ocg ? group * g.ocg + oc : 0;  // rows past the group read channel 0, never stored
-            const uint4 v = *reinterpret_cast<const uint4*>(wt + oc * g.kp + k0 + fk);
-            bf[j] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+            for (int j = 0; j < WN; ++j) {
+                int64_t oc = oc_base + j * 16 + fr;
+                oc = oc < g.ocg ? group * g.ocg + oc : 0;  // rows past the group read channel 0, never stored
+                const uint4 v = *reinterpret_cast<const uint4*>(wt + oc * g.kp + k0 + fk);
+                bf[j] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+            }
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < WM; ++i)
 #pragma unroll
-            for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < WN; ++j) {
+                const int64_t ocl = oc_base + j * 16 + fr;
+                if (ocl >= g.ocg) continue;
+                const int64_t oc = group * g.ocg + ocl;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t pix = pix_base + i * 16 + (lane >> 4) * 4 + r;
+                    if (pix >= np) continue;
+                    const int ohw = (int)(g.oh * g.ow), q = (int)pix;  // np < 2^31 (host-checked)
+                    const int64_t b = q / ohw;
+                    const int rem = q - (int)b * ohw;
+                    const int64_t oy = rem / (int)g.ow, ox = rem - (int)oy * (int)g.ow;
+                    const int32_t dot = acc[i][j][r] - (int32_t)g.zp_in * ep.wsum[oc];
+                    const int32_t total = dot + (bias ? bias[oc] : 0);
+                    const double real = (double)total * ((double)ep.s_a * (double)ep.w_scales[oc]);
+                    const int64_t off = g.layout == FHIP_NCHW ? ((b * (g.ocg * gridDim.z) + oc) * g.oh + oy) * g.ow + ox
+                                                              : ((b * g.oh + oy) * g.ow + ox) * (g.ocg * gridDim.z) + oc;
+                    ep.out[off] = requant_i8(real, ep.inv_out_den, ep.recip_out, ep.zp_out);
+                }
+            }
     }
-#pragma unroll
-    for (int i = 0; i < WM; ++i)
-#pragma unroll
-        for (int j = 0; j < WN; ++j) {
-            const int64_t ocl = oc_base + j * 16 + fr;
-            if (ocl >= g.ocg) continue;
-            const int64_t oc = group * g.ocg + ocl;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t pix = pix_base + i * 16 + (lane >> 4) * 4 + r;
-                if (pix >= np) continue;
-                const int ohw = (int)(g.oh * g.ow), q = (int)pix;  // np < 2^31 (host-checked)
-                const int64_t b = q / ohw;
-                const int rem = q - (int)b * ohw;
-                const int64_t oy = rem / (int)g.ow, ox = rem - (int)oy * (int)g.ow;
-                const int32_t dot = acc[i][j][r] - (int32_t)g.zp_in * ep.wsum[oc];
-                const int32_t total = dot + (bias ? bias[oc] : 0);
-                const double real = (double)total * ((double)ep.s_a * (double)ep.w_scales[oc]);
-                const int64_t off = g.layout == FHIP_NCHW ? ((b * (g.ocg * gridDim.z) + oc) * g.oh + oy) * g.ow + ox
-                                                          : ((b * g.oh + oy) * g.ow + ox) * (g.ocg * gridDim.z) + oc;
-                ep.out[off] = requant_i8(real, ep.inv_out_den, ep.recip_out, ep.zp_out);
+}
+
+// ---- INT8 Conv2D with one input channel per group (depthwise, channel multiplier ocg) -------------------
+// Direct: a thread per output element sums its kh*kw taps in int32 over the in-image positions (padding taps
+// are skipped, as the reference skips them: src/kernel/common/conv2d.cc:482-581), adds the bias and
+// requantizes like the other kernels.  Consecutive threads take consecutive output x (NCHW) or channels
+// (NHWC), so the output is written coalesced; the few input bytes per output come through the caches.
+// The host keeps the output element count below 2^31 (32-bit index splits).
+__global__ __launch_bounds__(256) void i8_conv_dw_kernel(const int8_t* __restrict__ in, ConvGeom g,
+                                                         const int8_t* __restrict__ wt,
+                                                         const int32_t* __restrict__ bias, I8Epilogue ep,
+                                                         int oc_total) {
+    const int ow = (int)g.ow, oh = (int)g.oh, w = (int)g.w, h = (int)g.h, kw = (int)g.kw, kh = (int)g.kh;
+    const int ocg = (int)g.ocg;
+    const int total = (int)g.n * oc_total * oh * ow;
+    for (int e = blockIdx.x * 256 + threadIdx.x; e < total; e += gridDim.x * 256) {
+        int b, oc, oy, ox, t;
+        if (g.layout == FHIP_NCHW) {
+            ox = e % ow;
+            t = e / ow;
+            oy = t % oh;
+            t /= oh;
+            oc = t % oc_total;
+            b = t / oc_total;
+        } else {
+            oc = e % oc_total;
+            t = e / oc_total;
+            ox = t % ow;
+            t /= ow;
+            oy = t % oh;
+            b = t / oh;
+        }
+        const int ci = oc / ocg;  // the group's one input channel
+        const int8_t* wrow = wt + (int64_t)oc * g.kp;
+        const int iy0 = oy * g.sh - g.ph, ix0 = ox * g.sw - g.pw;
+        int32_t acc = 0;
+        for (int ky = 0; ky < kh; ++ky) {
+            const int iy = iy0 + ky * g.dh;
+            if (iy < 0 || iy >= h) continue;
+            for (int kx = 0; kx < kw; ++kx) {
+                const int ix = ix0 + kx * g.dw;
+                if (ix < 0 || ix >= w) continue;
+                const int64_t off = g.layout == FHIP_NCHW ? (((int64_t)b * g.c + ci) * h + iy) * w + ix
+                                                          : (((int64_t)b * h + iy) * w + ix) * g.c + ci;
+                acc += ((int32_t)in[off] - (int32_t)g.zp_in) * (int32_t)wrow[ky * kw + kx];
             }
         }
+        const int32_t sum = acc + (bias ? bias[oc] : 0);
+        const double real = (double)sum * ((double)ep.s_a * (double)ep.w_scales[oc]);
+        ep.out[e] = requant_i8(real, ep.inv_out_den, ep.recip_out, ep.zp_out);
+    }
 }
 
 // ---- INT8 Conv2D, LDS-window implicit GEMM (group 1, IC a multiple of 64) -----------------------
@@ -889,12 +944,21 @@ int fhip_i8_conv2d(fhip_context ctx, const int8_t* in, int64_t n, int64_t c, int
             return FHIP_OK;
         }
     }
+    if (wt->icg == 1 && n * wt->n * oh * ow < (int64_t(1) << 31) && h * w < (int64_t(1) << 31)) {
+        const int64_t total = n * wt->n * oh * ow;
+        const unsigned grid = (unsigned)std::min<int64_t>((total + 255) / 256, 65536);
+        i8_conv_dw_kernel<<<grid, 256, 0, ctx->stream>>>(in, g, static_cast<const int8_t*>(wt->data), bias, ep,
+                                                         (int)wt->n);
+        ctx->last_backend = "i8_conv_depthwise";
+        FHIP_CHECK_LAUNCH(ctx, "i8_conv_dw_kernel");
+        return FHIP_OK;
+    }
     constexpr int WM = 2, WN = 2;
     const int64_t np = n * oh * ow;
-    if (np >= (int64_t(1) << 31) || h * w >= (int64_t(1) << 31) || (np + 32 * WM - 1) / (32 * WM) > 65535)
+    if (np >= (int64_t(1) << 31) || h * w >= (int64_t(1) << 31) || wt->group > 65535)
         return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "i8_conv2d: image too large for the gathered conv kernel");
-    dim3 grid((unsigned)((g.ocg + 32 * WN - 1) / (32 * WN)), (unsigned)((np + 32 * WM - 1) / (32 * WM)),
-              (unsigned)wt->group);
+    dim3 grid((unsigned)((g.ocg + 32 * WN - 1) / (32 * WN)),
+              (unsigned)std::min<int64_t>((np + 32 * WM - 1) / (32 * WM), 65535), (unsigned)wt->group);
     i8_conv_kernel<WM, WN><<<grid, 256, 0, ctx->stream>>>(in, g, static_cast<const int8_t*>(wt->data), bias, ep);
     ctx->last_backend = "i8_mfma_conv_64x64";
     FHIP_CHECK_LAUNCH(ctx, "i8_conv_kernel");

@@ -257,6 +257,55 @@ def test_i8_conv_requant_near_ties(ctx, sign):
 
 
 @pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("c,oc,group,kh,kw,stride,pad,dil", [
+    (24, 24, 24, 3, 3, (1, 1), (1, 1), (1, 1)),   # depthwise
+    (12, 24, 12, 3, 3, (2, 2), (1, 1), (1, 1)),   # channel multiplier 2, stride 2
+    (16, 16, 16, 5, 3, (1, 2), (2, 0), (2, 1)),   # asymmetric kernel, stride, pad and dilation
+    (1, 16, 1, 3, 3, (1, 1), (0, 1), (1, 1)),     # one input channel, group 1
+])
+def test_i8_conv_one_channel_per_group(ctx, layout, c, oc, group, kh, kw, stride, pad, dil):
+    """Convolutions whose groups hold one input channel (depthwise, channel multipliers, single-channel
+    inputs) run on the direct kernel; bit-exact against the oracle with a non-zero input zero point and bias."""
+    r = rng(61 + c + oc + kh)
+    n, h, wd = 2, 19, 23
+    x = r.integers(-128, 128, (n, c, h, wd)).astype(np.int8)
+    w = r.integers(-127, 128, (oc, c // group, kh, kw)).astype(np.int8)
+    s_w = r.uniform(1e-3, 1e-2, oc).astype(np.float32)
+    bias = r.integers(-3000, 3000, oc).astype(np.int32)
+    xl = x if layout == 0 else np.ascontiguousarray(x.transpose(0, 2, 3, 1))
+    rc, ref = po.i8_conv2d(xl, 0.04, -9, w, s_w, bias, stride, pad, 0.03, 5, dilation=dil, group=group,
+                           layout=layout)
+    assert rc == 0
+    wt = ctx.prepare_conv_weight(dev(w), s_w, group=group, version=9)
+    out = torch.empty(ref.shape, dtype=torch.int8, device="cuda")
+    ctx.i8_conv2d(dev(xl), layout, 0.04, -9, wt, out, 0.03, 5, stride=stride, pad=pad, dilation=dil,
+                  bias=dev(bias), bias_abs_max=3000)
+    assert ctx.last_backend() == "i8_conv_depthwise"
+    got = out.cpu().numpy()
+    assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatches"
+    wt.release()
+
+
+def test_i8_conv_general_path_large_image(ctx):
+    """The gathered conv kernel grid-strides its pixel tiles: a 2100 x 2100 output (68906 tiles of 64 pixels,
+    past the grid's 65535 y extent) on a grouped 1x1 conv with two input channels per group."""
+    r = rng(71)
+    n, c, h, wd, oc, g = 1, 4, 2100, 2100, 2, 2
+    x = r.integers(-128, 128, (n, c, h, wd)).astype(np.int8)
+    w = r.integers(-127, 128, (oc, c // g, 1, 1)).astype(np.int8)
+    s_w = r.uniform(1e-3, 1e-2, oc).astype(np.float32)
+    rc, ref = po.i8_conv2d(x, 0.05, 2, w, s_w, None, 1, 0, 0.01, -3, group=g)
+    assert rc == 0
+    wt = ctx.prepare_conv_weight(dev(w), s_w, group=g, version=10)
+    out = torch.empty(ref.shape, dtype=torch.int8, device="cuda")
+    ctx.i8_conv2d(dev(x), 0, 0.05, 2, wt, out, 0.01, -3)
+    assert ctx.last_backend() == "i8_mfma_conv_64x64"
+    got = out.cpu().numpy()
+    assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatches"
+    wt.release()
+
+
+@pytest.mark.parametrize("layout", [0, 1])
 def test_i8_conv_groups_dilation_zero_point(ctx, layout):
     r = rng(31)
     n, c, h, wd, oc, g = 2, 8, 13, 11, 12, 2
