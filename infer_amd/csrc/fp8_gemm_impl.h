@@ -25,6 +25,7 @@
 #ifndef FHIP_FP8_GEMM_IMPL_H
 #define FHIP_FP8_GEMM_IMPL_H
 #include "fp8_common.h"
+#include "i8_common.h"
 
 #include <cmath>
 #include <utility>
@@ -32,6 +33,9 @@
 namespace {
 
 using namespace fhip;
+
+typedef int v16i_t __attribute__((ext_vector_type(16)));
+typedef int v4i_t __attribute__((ext_vector_type(4)));
 
 
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [0, N).  Used where the accumulator
@@ -192,10 +196,17 @@ struct XcdMap {
 // WTN1 > 0 (WAVES_N == 2): the two wave columns are unequal, BN - WTN1 and WTN1 wide.  Waves w and
 // w + WAVES_M (one of each width) then share a SIMD (a block's waves are spread over the 4 SIMDs
 // round-robin), so every SIMD carries the same MFMA work; this lets BN be 224 = 128 + 96.
-template <bool E5, int BM, int BN, int WAVES_M, int WAVES_N, int OUT_BYTES, int SM, int BK, int STAGES, int WTN1>
+// I8 = true: the INT8 GEMM on the same tiles -- A and B are int8, each 64-deep step is two
+// v_mfma_i32_32x32x32_i8 (the two 16-byte halves of every lane's 32-byte K slice, for A and B alike, so
+// both still index the same K in every MFMA slot; integer sums are exact in any order), int32 accumulators,
+// and the epilogue is I8Epilogue's requantization (OUT_BYTES 1: INT8 codes, 4: fused DequantizeLinear to
+// FP32).  E5, SM and the Fp8Epilogue are unused then.
+template <bool E5, int BM, int BN, int WAVES_M, int WAVES_N, int OUT_BYTES, int SM, int BK, int STAGES, int WTN1,
+          bool I8 = false>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const uint8_t* __restrict__ a, int64_t m, int64_t k,
                                                        const uint8_t* __restrict__ b, int64_t kp, int64_t np,
-                                                       int tiles_n, int tiles_total, XcdMap xm, int mfma_scale, Fp8Epilogue ep) {
+                                                       int tiles_n, int tiles_total, XcdMap xm, int mfma_scale, Fp8Epilogue ep,
+                                                       I8Epilogue iep) {
     constexpr int NT = 64 * WAVES_M * WAVES_N;
     using S = Stage<BM, BN, NT, BK>;
     constexpr int kSub = BK / 64;  // 64-deep MFMA steps per stage
@@ -266,13 +277,14 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
   // The rest runs with this wave's fragment-column count FN as a compile-time constant.
   auto body = [&](auto fn_tag) {
     constexpr int FN = decltype(fn_tag)::value;
-    v16f acc[FM][FN];
+    using AccT = std::conditional_t<I8, v16i_t, v16f>;
+    AccT acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
 
     const int frag_row = lane & 31;
     const int frag_c = (lane >> 5) * 2;
@@ -310,12 +322,22 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
-                const v8i av = v8i{(int)fa[i][0].x, (int)fa[i][0].y, (int)fa[i][0].z, (int)fa[i][0].w,
-                                   (int)fa[i][1].x, (int)fa[i][1].y, (int)fa[i][1].z, (int)fa[i][1].w};
-                const v8i bv = v8i{(int)fb[j][0].x, (int)fb[j][0].y, (int)fb[j][0].z, (int)fb[j][0].w,
-                                   (int)fb[j][1].x, (int)fb[j][1].y, (int)fb[j][1].z, (int)fb[j][1].w};
-                // weight fragment as the row operand: each 32x32 block is computed transposed
-                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[i][j], fmt, fmt, 0, scale_v, 0, 127);
+                if constexpr (I8) {
+                    // weight fragment as the row operand: each 32x32 block is computed transposed
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const v4i_t av = v4i_t{(int)fa[i][h].x, (int)fa[i][h].y, (int)fa[i][h].z, (int)fa[i][h].w};
+                        const v4i_t bv = v4i_t{(int)fb[j][h].x, (int)fb[j][h].y, (int)fb[j][h].z, (int)fb[j][h].w};
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bv, av, acc[i][j], 0, 0, 0);
+                    }
+                } else {
+                    const v8i av = v8i{(int)fa[i][0].x, (int)fa[i][0].y, (int)fa[i][0].z, (int)fa[i][0].w,
+                                       (int)fa[i][1].x, (int)fa[i][1].y, (int)fa[i][1].z, (int)fa[i][1].w};
+                    const v8i bv = v8i{(int)fb[j][0].x, (int)fb[j][0].y, (int)fb[j][0].z, (int)fb[j][0].w,
+                                       (int)fb[j][1].x, (int)fb[j][1].y, (int)fb[j][1].z, (int)fb[j][1].w};
+                    // weight fragment as the row operand: each 32x32 block is computed transposed
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[i][j], fmt, fmt, 0, scale_v, 0, 127);
+                }
             }
         // Pin the MFMAs here: they are pure operations, which IR-level code motion may sink below the
         // following lgkmcnt fence (sched_barrier binds only the machine scheduler).  Volatile asm keeps
@@ -430,8 +452,47 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
             stage_tile(bias_tag, std::true_type{});
         }
     };
-    if (ep.bias_kind != FHIP_BIAS_NONE) epilogue(std::true_type{});
-    else epilogue(std::false_type{});
+    if constexpr (I8) {
+        // INT8: each value's requantized code (I8Epilogue: zero-point correction, bias, alpha/beta, scales,
+        // exact rounding), then the code itself (OUT_BYTES 1) or its DequantizeLinear value (2: FP16/BF16,
+        // 4: FP32).  Positions past m or n are never stored; they are not evaluated either, so a bias is
+        // read only inside the output.
+        static_for<FM * FN>([&](auto ij) {
+            constexpr int i = decltype(ij)::value / FN, j = decltype(ij)::value % FN;
+            static_for<4>([&](auto gg) {
+                constexpr int g = decltype(gg)::value;
+                const int r = wm * WTM + i * 32 + row_in;
+                const int c = wcol + j * 32 + g * 8 + col_q;
+                const int64_t row = m0 + r, col = n0 + c;
+                int8_t q[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    q[t] = row < m && col + t < iep.ldo
+                               ? iep.code(acc[i][j][4 * g + t], row, col + t, iep.col_params(col + t))
+                               : int8_t(0);
+                uint8_t* dst = so + r * kOutPitch + c * OUT_BYTES;
+                if constexpr (OUT_BYTES == 1) {
+                    *reinterpret_cast<uint32_t*>(dst) = (uint32_t)(uint8_t)q[0] | (uint32_t)(uint8_t)q[1] << 8 |
+                                                        (uint32_t)(uint8_t)q[2] << 16 | (uint32_t)(uint8_t)q[3] << 24;
+                } else if constexpr (OUT_BYTES == 2) {
+                    uint16_t h[4];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const float v = iep.dequant(q[t]);
+                        h[t] = iep.out_dtype == FHIP_FP16 ? fhip::fp16_encode(v) : fhip::bf16_encode_plain(v);
+                    }
+                    *reinterpret_cast<uint2*>(dst) = make_uint2((uint32_t)h[0] | (uint32_t)h[1] << 16,
+                                                                (uint32_t)h[2] | (uint32_t)h[3] << 16);
+                } else {
+                    *reinterpret_cast<float4*>(dst) =
+                        make_float4(iep.dequant(q[0]), iep.dequant(q[1]), iep.dequant(q[2]), iep.dequant(q[3]));
+                }
+            });
+        });
+    } else {
+        if (ep.bias_kind != FHIP_BIAS_NONE) epilogue(std::true_type{});
+        else epilogue(std::false_type{});
+    }
   };
     // wave-uniform branch; both bodies run the same sequence of barriers
     if (WTN1 == 0 || wn == 0) body(std::integral_constant<int, FN0>{});
@@ -463,9 +524,10 @@ constexpr size_t lds_bytes() {
     return ops > epi ? ops : epi;
 }
 
-template <bool E5, int OB, int BM, int BN, int WAVES_M, int WAVES_N, int BK = 64, int STAGES = 4, int WTN1 = 0>
+template <bool E5, int OB, int BM, int BN, int WAVES_M, int WAVES_N, int BK = 64, int STAGES = 4, int WTN1 = 0,
+          bool I8 = false>
 int launch_tile(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, const fhip_weight_s* w,
-                const Fp8Epilogue& ep, const char* name) {
+                const Fp8Epilogue& ep, const char* name, const I8Epilogue* iep = nullptr) {
     const int64_t kp = ((w->k + 127) / 128) * 128;
     const int64_t np = ((w->n + 255) / 256) * 256;
     const int tiles_m = (int)((m + BM - 1) / BM), tiles_n = (int)((w->n + BN - 1) / BN);
@@ -501,9 +563,9 @@ int launch_tile(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, cons
         }
     }
 #define FHIP_GEMM_LAUNCH(OB, SMV)                                                                                   \
-    fp8_gemm_kernel<E5, BM, BN, WAVES_M, WAVES_N, OB, SMV, BK, STAGES, WTN1><<<grid, 64 * WAVES_M * WAVES_N,                           \
+    fp8_gemm_kernel<E5, BM, BN, WAVES_M, WAVES_N, OB, SMV, BK, STAGES, WTN1, I8><<<grid, 64 * WAVES_M * WAVES_N,                       \
                                                           lds_bytes<BM, BN, 64 * WAVES_M * WAVES_N, OB, BK, STAGES>(), ctx->stream>>>( \
-        a, m, k64, wd, kp, np, tiles_n, tiles, xm, mfma_scale, ep)
+        a, m, k64, wd, kp, np, tiles_n, tiles, xm, mfma_scale, ep, iep ? *iep : I8Epilogue{})
 #define FHIP_GEMM_LAUNCH_SM(OB)                                                                                     \
     do {                                                                                                            \
         if (sm == kScaleFolded) FHIP_GEMM_LAUNCH(OB, kScaleFolded);                                                 \
@@ -512,6 +574,8 @@ int launch_tile(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, cons
     } while (0)
     if constexpr (lds_bytes<BM, BN, 64 * WAVES_M * WAVES_N, OB, BK, STAGES>() > 160 * 1024) {
         return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "fp8 gemm: output tile too large for LDS");
+    } else if constexpr (I8) {
+        FHIP_GEMM_LAUNCH(OB, kScaleGeneral);
     } else {
         FHIP_GEMM_LAUNCH_SM(OB);
     }

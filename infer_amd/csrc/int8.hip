@@ -16,99 +16,21 @@
 //     q    = clamp(round_half_away(real / double(s_out) + zp_out), -128, 127)
 #include "fhip_internal.h"
 #include "codec.h"
+#include "i8_common.h"
 
 #include <algorithm>
 #include <cmath>
 
 namespace {
 
+using fhip::I8Epilogue;
+using fhip::clamp_round_i8;
+using fhip::requant_i8;
+using fhip::requant_i8_fast;
+
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 #pragma clang fp contract(off)
-
-__device__ __forceinline__ int8_t clamp_round_i8(double t) {
-    const double r = round(t);
-    const double hi = (r < 127.0) ? r : 127.0;      // std::min(127.0, r): NaN -> 127
-    const double lo = (-128.0 < hi) ? hi : -128.0;  // std::max(-128.0, hi)
-    return (int8_t)lo;
-}
-
-// clamp_round_i8(real / s_out + zp_out), the reference's requantization (int8_kernel_utils.h:155-179),
-// without a double division on the common path.  t = real * (1 / s_out) + zp_out differs from the divided
-// form by at most ~2^-51 * (|t| + |zp_out|) (the reciprocal and the product are each correctly rounded);
-// round() changes value only at the x.5 points, so wherever t is farther than that from one both forms
-// round to the same integer.  Only near an x.5 point (or for non-finite t) is the division done.
-__device__ __forceinline__ int8_t requant_i8_fast(double real, double recip_out, double zp_out, bool& near_tie) {
-    const double t = real * recip_out + zp_out;
-    const double half_gap = fabs((t - floor(t)) - 0.5);
-    near_tie = !(half_gap > 0x1p-40 * (fabs(t) + 256.0));
-    return clamp_round_i8(t);
-}
-__device__ __forceinline__ int8_t requant_i8(double real, double s_out, double recip_out, double zp_out) {
-    bool near_tie;
-    const int8_t q = requant_i8_fast(real, recip_out, zp_out, near_tie);
-    if (near_tie) return clamp_round_i8(real / s_out + zp_out);
-    return q;
-}
-
-struct I8Epilogue {
-    int kind;
-    const float* w_scales;   // [n] (per-tensor weights: all equal)
-    const int32_t* wsum;     // [n]
-    const int32_t* bias;
-    int bias_kind;
-    int32_t zp_a;
-    float s_a;
-    double alpha, beta;
-    double inv_out_den;      // double(s_out), used as a divisor
-    double zp_out;
-    double recip_out;        // 1 / double(s_out), for requant_i8
-    int8_t* out;
-    int64_t ldo;
-    // Fused DequantizeLinear (per tensor): out_dtype FP32/FP16/BF16 writes float((q - dq_zp) * dq_scale) with
-    // DequantizeLinear's own encoders into out_any instead of the INT8 code q into out.
-    int out_dtype = FHIP_INT8;
-    float dq_scale = 1.0f;
-    int32_t dq_zp = 0;
-    void* out_any = nullptr;
-
-    // Per-output-channel parameters, loadable ahead of the main loop.
-    struct Col {
-        int32_t wsum;
-        int32_t bias;  // vector bias (0 without one; a matrix bias is read per element)
-        float w_scale;
-    };
-    __device__ __forceinline__ Col col_params(int64_t col) const {
-        return Col{wsum[col], bias_kind == FHIP_BIAS_VECTOR ? bias[col] : 0, w_scales[col]};
-    }
-
-    __device__ __forceinline__ void store(int32_t raw, int64_t row, int64_t col) const {
-        store(raw, row, col, col_params(col));
-    }
-
-    __device__ __forceinline__ void store(int32_t raw, int64_t row, int64_t col, const Col& c) const {
-        const int32_t dot = raw - zp_a * c.wsum;
-        const int32_t b = bias_kind == FHIP_BIAS_MATRIX ? bias[row * ldo + col] : c.bias;
-        const double scale = (double)s_a * (double)c.w_scale;
-        double real;
-        if (kind == FHIP_I8_GEMM) {
-            const double acc = alpha * (double)dot + beta * (double)b;
-            real = acc * scale;
-        } else {
-            real = (double)(dot + b) * scale;  // MatMul has no bias (b = 0)
-        }
-        const int8_t q = requant_i8(real, inv_out_den, recip_out, zp_out);
-        const int64_t idx = row * ldo + col;
-        if (out_dtype == FHIP_INT8) {
-            out[idx] = q;
-        } else {
-            const float v = (float)((int32_t)q - dq_zp) * dq_scale;  // quantize_linear_utils.h:291-341
-            if (out_dtype == FHIP_FP32) static_cast<float*>(out_any)[idx] = v;
-            else if (out_dtype == FHIP_FP16) static_cast<uint16_t*>(out_any)[idx] = fhip::fp16_encode(v);
-            else static_cast<uint16_t*>(out_any)[idx] = fhip::bf16_encode_plain(v);
-        }
-    }
-};
 
 // ---- INT8 GEMM: A [m][k] int8 row-major, B prepared [Np][Kp] ---------------------------------
 // Block tile (16*FM) x (16*FN).  The NW waves split K: wave w takes the 64-deep steps w, w+NW, ...,
@@ -116,6 +38,8 @@ struct I8Epilogue {
 // NW partial tiles are summed through LDS; integer sums are exact in any order.
 // MFMA depth 64: lane l supplies row/col l%16 and bytes [16*(l/16), 16*(l/16)+16) of the step.
 constexpr int kI8Unroll = 4;
+// From this many activation rows on, fhip_i8_linear runs the tile GEMM (i8_gemm_tile.hip) instead.
+constexpr int64_t kI8TileMinRows = 256;
 
 template <int FM, int FN, int NW = 4, int UNR = kI8Unroll>
 __global__ __launch_bounds__(NW * 64) void i8_gemm_kernel(const int8_t* __restrict__ a, int64_t m, int64_t k,
@@ -869,6 +793,10 @@ int fhip_i8_linear_ex(fhip_context ctx, int kind, const int8_t* a, float s_a, in
     ep.dq_scale = dq_scale;
     ep.dq_zp = dq_zp;
     ep.out_any = out;
+    // Large M: the LDS-staged MFMA tile GEMM (operand reuse across a 128x128 or 256x256 tile).
+    if (m >= kI8TileMinRows && w->k % 64 == 0 && (reinterpret_cast<uintptr_t>(a) & 15) == 0 &&
+        m * w->k < (int64_t(1) << 31))
+        return fhip::launch_i8_gemm_tile(ctx, a, m, w, ep);
     const int64_t kp = ((w->k + 127) / 128) * 128;
     // largest tile that still puts about two blocks on every CU
     const int64_t blocks32 = ((w->n + 31) / 32) * ((m + 31) / 32);

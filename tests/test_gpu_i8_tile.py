@@ -1,0 +1,108 @@
+"""GPU parity of the INT8 linear's large-M path (the MFMA tile GEMM in its INT8 mode): bit-exact against the
+oracle for Gemm / FC / MatMul, both weight layouts, zero points, vector and matrix bias, alpha/beta, ragged M
+and N, both stage depths (K a multiple of 128, or of 64 only), both tile sizes, exact requantization ties
+(power-of-two scales) and the fused DequantizeLinear outputs."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import pyoracle as po
+from tests.common import rng
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a).cuda()
+
+
+CASES = [
+    # m, k, n, kind, bias_kind, zp_a, zp_y, alpha, beta, pow2 scales, backend
+    (512, 1024, 1024, po.I8_GEMM, po.BIAS_VECTOR, 0, 0, 1.0, 1.0, False, "i8_mfma_gemm_128x128_bk128_w8"),
+    (300, 192, 700, po.I8_GEMM, po.BIAS_MATRIX, -20, 10, 0.75, -1.5, True, "i8_mfma_gemm_128x128_w8"),
+    (3000, 256, 4000, po.I8_GEMM, po.BIAS_VECTOR, 7, -4, 1.0, 1.0, False, "i8_mfma_gemm_256x256_bk128_w8"),
+    (3100, 320, 3900, po.I8_FC, po.BIAS_VECTOR, -3, 2, 1.0, 1.0, True, "i8_mfma_gemm_256x256_w8"),
+    (257, 128, 33, po.I8_MATMUL, po.BIAS_NONE, 12, 0, 1.0, 1.0, False, "i8_mfma_gemm_128x128_bk128_w8"),
+    (777, 64, 515, po.I8_GEMM, po.BIAS_NONE, 0, -1, 2.0, 0.0, True, "i8_mfma_gemm_128x128_w8"),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}x{c[1]}x{c[2]}_k{c[3]}" for c in CASES])
+def test_i8_tile_gemm_bitexact(ctx, case):
+    m, k, n, kind, bias_kind, zp_a, zp_y, alpha, beta, pow2, backend = case
+    r = rng(m * 7 + n)
+    xq = r.integers(-128, 128, (m, k)).astype(np.int8)
+    w = r.integers(-127, 128, (n, k)).astype(np.int8)
+    if pow2:
+        s_w = np.full(n, 2.0 ** -8, np.float32)
+        s_x, s_y = 0.0625, 2.0
+    else:
+        s_w = r.uniform(1e-3, 1e-2, n).astype(np.float32)
+        s_x, s_y = 0.02, 0.4
+    bias = None
+    if bias_kind == po.BIAS_VECTOR:
+        bias = r.integers(-20000, 20000, n).astype(np.int32)
+    elif bias_kind == po.BIAS_MATRIX:
+        bias = r.integers(-3000, 3000, (m, n)).astype(np.int32)
+    trans_b = kind == po.I8_GEMM
+    w_src = w if trans_b else np.ascontiguousarray(w.T)
+    rc, ref, _ = po.i8_linear(kind, xq, s_x, zp_a, w_src, trans_b, s_w, None, bias, bias_kind, alpha, beta, s_y, zp_y)
+    assert rc == 0
+    wt = ctx.prepare_weight(dev(w_src), po.INT8, k, n, 1 if trans_b else 0, scales=s_w, version=300 + m)
+    out = torch.empty((m, n), dtype=torch.int8, device="cuda")
+    kw = {}
+    if bias is not None:
+        kw = dict(bias=dev(bias), bias_kind=bias_kind, bias_abs_max=int(np.abs(bias).max()))
+    ctx.i8_linear(kind, dev(xq), s_x, zp_a, m, wt, out, s_y, zp_y, alpha=alpha, beta=beta, **kw)
+    got = out.cpu().numpy()
+    assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatches ({ctx.last_backend()})"
+    assert ctx.last_backend() == backend
+    wt.release()
+
+
+@pytest.mark.parametrize("out_dtype", [po.FP32, po.FP16, po.BF16])
+@pytest.mark.parametrize("m,k,n", [(600, 512, 1000), (2048, 256, 3000)])
+def test_i8_tile_gemm_fused_dequantize(ctx, out_dtype, m, k, n):
+    r = rng(m + n + out_dtype)
+    xq = r.integers(-128, 128, (m, k)).astype(np.int8)
+    w = r.integers(-127, 128, (n, k)).astype(np.int8)
+    s_w = r.uniform(1e-3, 1e-2, n).astype(np.float32)
+    bias = r.integers(-20000, 20000, n).astype(np.int32)
+    s_x, s_y, zp_y, s_dq, zp_dq = 0.02, 0.0371, -6, 0.0125, 3
+    rc, yq, _ = po.i8_linear(po.I8_GEMM, xq, s_x, 0, w, True, s_w, None, bias, po.BIAS_VECTOR, 1.0, 1.0, s_y, zp_y)
+    assert rc == 0
+    rc, ref = po.dequantize_linear(yq, [s_dq], [zp_dq], out_dtype)
+    assert rc == 0
+    wt = ctx.prepare_weight(dev(w), po.INT8, k, n, 1, scales=s_w, version=400 + m)
+    tdt = torch.float32 if out_dtype == po.FP32 else torch.int16
+    out = torch.empty((m, n), dtype=tdt, device="cuda")
+    ctx.i8_linear_ex(po.I8_GEMM, dev(xq), s_x, 0, m, wt, out, out_dtype, s_y, zp_y, dq_scale=s_dq, dq_zp=zp_dq,
+                     bias=dev(bias), bias_kind=po.BIAS_VECTOR, bias_abs_max=20000)
+    assert ctx.last_backend().startswith("i8_mfma_gemm_")
+    got = out.cpu().numpy()
+    if out_dtype != po.FP32:
+        got = got.view(np.uint16)
+    assert np.array_equal(got.view(np.uint8), np.ascontiguousarray(ref).view(np.uint8))
+    wt.release()
+
+
+def test_i8_tile_gemm_unaligned_activation_uses_small_tiles(ctx):
+    """An activation pointer off 16-byte alignment keeps the K-split kernels, with the same result."""
+    r = rng(77)
+    m, k, n = 512, 256, 256
+    buf = r.integers(-128, 128, m * k + 16).astype(np.int8)
+    w = r.integers(-127, 128, (n, k)).astype(np.int8)
+    s_w = r.uniform(1e-3, 1e-2, n).astype(np.float32)
+    xq = buf[1:1 + m * k].reshape(m, k)
+    rc, ref, _ = po.i8_linear(po.I8_GEMM, xq, 0.02, 0, w, True, s_w, None, None, po.BIAS_NONE, 1.0, 1.0, 0.4, 0)
+    assert rc == 0
+    wt = ctx.prepare_weight(dev(w), po.INT8, k, n, 1, scales=s_w, version=500)
+    dbuf = dev(buf)
+    out = torch.empty((m, n), dtype=torch.int8, device="cuda")
+    ctx.i8_linear(po.I8_GEMM, dbuf[1:1 + m * k].view(m, k), 0.02, 0, m, wt, out, 0.4, 0)
+    assert ctx.last_backend().endswith("_ksplit4")
+    assert np.array_equal(out.cpu().numpy(), ref)
+    wt.release()
