@@ -67,6 +67,16 @@ struct Stage {
     static_assert(kLoadsA * NT == BM * kChunks, "BM must be a multiple of NT/kChunks");
 };
 
+// Dynamic LDS of the tile kernel: the operand stage ring, reused for the output tile in the epilogue;
+// in the INT8 mode followed by the tile's per-column requantization parameters (wsum, vector bias, weight
+// scale: three [BN] arrays of 4-byte values).
+template <int BM, int BN, int NT, int OUT_BYTES, int BK, int STAGES, bool I8 = false>
+constexpr size_t lds_bytes() {
+    constexpr size_t ops = (size_t)STAGES * Stage<BM, BN, NT, BK>::kBytes;
+    constexpr size_t epi = (size_t)BM * (BN * OUT_BYTES + 16);
+    return (ops > epi ? ops : epi) + (I8 ? (size_t)BN * 12 : 0);
+}
+
 template <int BK>
 __device__ __forceinline__ int swz(int r) { return BK == 64 ? (r >> 2) & 3 : (r >> 1) & 7; }
 
@@ -274,6 +284,25 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
 
     constexpr int kOutPitch = BN * OUT_BYTES + 16;  // epilogue: output tile staged in LDS
     uint8_t* const so = smem;
+    // INT8: the tile's per-column requantization parameters move to LDS (past the ring and the output tile)
+    // with 4-byte buffer_load ... lds, issued before any stage load: every later vmcnt wait of the main
+    // loop covers them.  Columns past n read as zero and are never stored.
+    constexpr size_t kColOff = lds_bytes<BM, BN, NT, OUT_BYTES, BK, STAGES, false>();
+    if constexpr (I8) {
+        static_assert(BN % 64 == 0, "INT8 mode: BN a multiple of 64");
+        constexpr int kParts = BN / 64;
+        const int cols = (int)(iep.ldo - n0 < BN ? iep.ldo - n0 : BN);
+        for (int q = wave; q < 3 * kParts; q += NT / 64) {
+            const int arr = q / kParts, part = q % kParts;
+            const void* src = arr == 0 ? (const void*)iep.wsum
+                              : arr == 1 ? (const void*)iep.bias : (const void*)iep.w_scales;
+            const int bytes = arr == 1 && iep.bias_kind != FHIP_BIAS_VECTOR ? 0 : cols * 4;
+            const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+                (void*)(static_cast<const uint8_t*>(src) + (bytes ? n0 * 4 : 0)), 0, bytes, kBufferRsrcWord3);
+            uint8_t* dst = smem + kColOff + (size_t)arr * BN * 4 + part * 256;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 4, (uint32_t)(part * 256 + lane * 4), 0, 0, 0);
+        }
+    }
   // The rest runs with this wave's fragment-column count FN as a compile-time constant.
   auto body = [&](auto fn_tag) {
     constexpr int FN = decltype(fn_tag)::value;
@@ -411,6 +440,21 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
             mfmas(fa, fb);
         }
     }
+    if constexpr (I8) {
+        // Integer path: each column's parameters become (dot + bias correction, kl, kh) in place: shift =
+        // vector bias - zp_a * wsum, and K = s_a * s_w / s_out split into a float pair.  The staged values
+        // are visible here (every wave waited for its loads and passed a barrier since).
+        if (iep.int_path) {
+            int32_t* cw = reinterpret_cast<int32_t*>(smem + kColOff);
+            for (int c = tid; c < BN; c += NT) {
+                float kh, kl;
+                iep.split_scale(reinterpret_cast<const float*>(cw + 2 * BN)[c], kh, kl);
+                cw[c] = (iep.bias_kind == FHIP_BIAS_VECTOR ? cw[BN + c] : 0) - iep.zp_a * cw[c];
+                reinterpret_cast<float*>(cw + BN)[c] = kl;
+                reinterpret_cast<float*>(cw + 2 * BN)[c] = kh;
+            }
+        }
+    }
     __syncthreads();
 
     // ---- epilogue.  The MFMA computed each 32x32 block transposed (weight fragment as the row operand),
@@ -453,42 +497,100 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
         }
     };
     if constexpr (I8) {
-        // INT8: each value's requantized code (I8Epilogue: zero-point correction, bias, alpha/beta, scales,
-        // exact rounding), then the code itself (OUT_BYTES 1) or its DequantizeLinear value (2: FP16/BF16,
-        // 4: FP32).  Positions past m or n are never stored; they are not evaluated either, so a bias is
-        // read only inside the output.
-        static_for<FM * FN>([&](auto ij) {
-            constexpr int i = decltype(ij)::value / FN, j = decltype(ij)::value % FN;
-            static_for<4>([&](auto gg) {
-                constexpr int g = decltype(gg)::value;
-                const int r = wm * WTM + i * 32 + row_in;
-                const int c = wcol + j * 32 + g * 8 + col_q;
-                const int64_t row = m0 + r, col = n0 + c;
-                int8_t q[4];
-#pragma unroll
-                for (int t = 0; t < 4; ++t)
-                    q[t] = row < m && col + t < iep.ldo
-                               ? iep.code(acc[i][j][4 * g + t], row, col + t, iep.col_params(col + t))
-                               : int8_t(0);
-                uint8_t* dst = so + r * kOutPitch + c * OUT_BYTES;
-                if constexpr (OUT_BYTES == 1) {
-                    *reinterpret_cast<uint32_t*>(dst) = (uint32_t)(uint8_t)q[0] | (uint32_t)(uint8_t)q[1] << 8 |
-                                                        (uint32_t)(uint8_t)q[2] << 16 | (uint32_t)(uint8_t)q[3] << 24;
-                } else if constexpr (OUT_BYTES == 2) {
-                    uint16_t h[4];
+        // INT8: each value's requantized code (I8Epilogue: zero-point correction, bias, alpha/beta, scales),
+        // then the code itself (OUT_BYTES 1) or its DequantizeLinear value (2: FP16/BF16, 4: FP32).  The hot
+        // pass decides every code in fp32 (requant_i8_f32's error bound) and flags, one bit per value, those
+        // it cannot decide (near an x.5 point).  Positions past m or n are never stored and not evaluated, so
+        // a bias is read only inside the output.
+        constexpr int kElems = FM * FN * 16;
+        uint32_t unsafe_bits[(kElems + 31) / 32] = {};
+        uint32_t any_unsafe = 0;
+        const int32_t zp_out_i = (int32_t)iep.zp_out;
+        auto hot = [&](auto int_tag) __attribute__((always_inline)) {
+            constexpr bool INT = decltype(int_tag)::value;
+            static_for<FM * FN>([&](auto ij) {
+                constexpr int i = decltype(ij)::value / FN, j = decltype(ij)::value % FN;
+                static_for<4>([&](auto gg) {
+                    constexpr int g = decltype(gg)::value;
+                    constexpr int e0 = (decltype(ij)::value * 4 + g) * 4;
+                    const int r = wm * WTM + i * 32 + row_in;
+                    const int c = wcol + j * 32 + g * 8 + col_q;
+                    const int64_t row = m0 + r, col = n0 + c;
+                    const uint8_t* cp = smem + kColOff + c * 4;
+                    const int4 p0 = *reinterpret_cast<const int4*>(cp);
+                    const int4 p1 = *reinterpret_cast<const int4*>(cp + BN * 4);
+                    const float4 p2 = *reinterpret_cast<const float4*>(cp + BN * 8);
+                    const int a0[4] = {p0.x, p0.y, p0.z, p0.w}, a1[4] = {p1.x, p1.y, p1.z, p1.w};
+                    const float a2[4] = {p2.x, p2.y, p2.z, p2.w};
+                    int8_t q[4];
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
-                        const float v = iep.dequant(q[t]);
-                        h[t] = iep.out_dtype == FHIP_FP16 ? fhip::fp16_encode(v) : fhip::bf16_encode_plain(v);
+                        q[t] = 0;
+                        if (row < m && col + t < iep.ldo) {
+                            bool unsafe;
+                            if constexpr (INT) {
+                                // a0 = shift, a1 = kl bits, a2 = kh
+                                int32_t v = acc[i][j][4 * g + t] + a0[t];
+                                if (iep.bias_kind == FHIP_BIAS_MATRIX) v += iep.bias[row * iep.ldo + col + t];
+                                q[t] = requant_i8_split(v, a2[t], __int_as_float(a1[t]), zp_out_i, unsafe);
+                            } else {
+                                const I8Epilogue::Col cpt{a0[t], a1[t], a2[t]};
+                                const double v = iep.real(acc[i][j][4 * g + t], row, col + t, cpt);
+                                q[t] = requant_i8_fast(v, iep.recip_out, iep.zp_out, unsafe);
+                            }
+                            unsafe_bits[(e0 + t) / 32] |= (uint32_t)unsafe << ((e0 + t) % 32);
+                            any_unsafe |= (uint32_t)unsafe;
+                        }
                     }
-                    *reinterpret_cast<uint2*>(dst) = make_uint2((uint32_t)h[0] | (uint32_t)h[1] << 16,
-                                                                (uint32_t)h[2] | (uint32_t)h[3] << 16);
-                } else {
-                    *reinterpret_cast<float4*>(dst) =
-                        make_float4(iep.dequant(q[0]), iep.dequant(q[1]), iep.dequant(q[2]), iep.dequant(q[3]));
-                }
+                    uint8_t* dst = so + r * kOutPitch + c * OUT_BYTES;
+                    if constexpr (OUT_BYTES == 1) {
+                        *reinterpret_cast<uint32_t*>(dst) = (uint32_t)(uint8_t)q[0] | (uint32_t)(uint8_t)q[1] << 8 |
+                                                            (uint32_t)(uint8_t)q[2] << 16 | (uint32_t)(uint8_t)q[3] << 24;
+                    } else if constexpr (OUT_BYTES == 2) {
+                        uint16_t h[4];
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+                            const float v = iep.dequant(q[t]);
+                            h[t] = iep.out_dtype == FHIP_FP16 ? fhip::fp16_encode(v) : fhip::bf16_encode_plain(v);
+                        }
+                        *reinterpret_cast<uint2*>(dst) = make_uint2((uint32_t)h[0] | (uint32_t)h[1] << 16,
+                                                                    (uint32_t)h[2] | (uint32_t)h[3] << 16);
+                    } else {
+                        *reinterpret_cast<float4*>(dst) =
+                            make_float4(iep.dequant(q[0]), iep.dequant(q[1]), iep.dequant(q[2]), iep.dequant(q[3]));
+                    }
+                });
             });
-        });
+        };
+        if (iep.int_path) hot(std::true_type{});
+        else hot(std::false_type{});
+        // Cold pass: only the flagged values are recomputed with the reference's fp64 arithmetic (column
+        // parameters from global memory: the integer path rewrote the staged ones) and patched into the
+        // staged tile (same thread, same LDS bytes).
+        if (__builtin_expect(any_unsafe != 0, 0)) {
+            static_for<FM * FN>([&](auto ij) {
+                constexpr int i = decltype(ij)::value / FN, j = decltype(ij)::value % FN;
+                static_for<16>([&](auto ee) {
+                    constexpr int e = decltype(ee)::value, g = e / 4, t = e % 4;
+                    constexpr int bit = decltype(ij)::value * 16 + e;
+                    if (unsafe_bits[bit / 32] & (1u << (bit % 32))) {
+                        const int r = wm * WTM + i * 32 + row_in;
+                        const int c = wcol + j * 32 + g * 8 + col_q + t;
+                        const int8_t q = iep.code(acc[i][j][e], m0 + r, n0 + c, iep.col_params(n0 + c));
+                        uint8_t* dst = so + r * kOutPitch + c * OUT_BYTES;
+                        if constexpr (OUT_BYTES == 1) {
+                            *reinterpret_cast<int8_t*>(dst) = q;
+                        } else if constexpr (OUT_BYTES == 2) {
+                            const float v = iep.dequant(q);
+                            *reinterpret_cast<uint16_t*>(dst) =
+                                iep.out_dtype == FHIP_FP16 ? fhip::fp16_encode(v) : fhip::bf16_encode_plain(v);
+                        } else {
+                            *reinterpret_cast<float*>(dst) = iep.dequant(q);
+                        }
+                    }
+                });
+            });
+        }
     } else {
         if (ep.bias_kind != FHIP_BIAS_NONE) epilogue(std::true_type{});
         else epilogue(std::false_type{});
@@ -517,12 +619,6 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
     }
 }
 
-template <int BM, int BN, int NT, int OUT_BYTES, int BK, int STAGES>
-constexpr size_t lds_bytes() {
-    constexpr size_t ops = (size_t)STAGES * Stage<BM, BN, NT, BK>::kBytes;
-    constexpr size_t epi = (size_t)BM * (BN * OUT_BYTES + 16);
-    return ops > epi ? ops : epi;
-}
 
 template <bool E5, int OB, int BM, int BN, int WAVES_M, int WAVES_N, int BK = 64, int STAGES = 4, int WTN1 = 0,
           bool I8 = false>
@@ -564,7 +660,7 @@ int launch_tile(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, cons
     }
 #define FHIP_GEMM_LAUNCH(OB, SMV)                                                                                   \
     fp8_gemm_kernel<E5, BM, BN, WAVES_M, WAVES_N, OB, SMV, BK, STAGES, WTN1, I8><<<grid, 64 * WAVES_M * WAVES_N,                       \
-                                                          lds_bytes<BM, BN, 64 * WAVES_M * WAVES_N, OB, BK, STAGES>(), ctx->stream>>>( \
+                                                          lds_bytes<BM, BN, 64 * WAVES_M * WAVES_N, OB, BK, STAGES, I8>(), ctx->stream>>>( \
         a, m, k64, wd, kp, np, tiles_n, tiles, xm, mfma_scale, ep, iep ? *iep : I8Epilogue{})
 #define FHIP_GEMM_LAUNCH_SM(OB)                                                                                     \
     do {                                                                                                            \
@@ -572,7 +668,7 @@ int launch_tile(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, cons
         else if (sm == kScalePow2) FHIP_GEMM_LAUNCH(OB, kScalePow2);                                                \
         else FHIP_GEMM_LAUNCH(OB, kScaleGeneral);                                                                   \
     } while (0)
-    if constexpr (lds_bytes<BM, BN, 64 * WAVES_M * WAVES_N, OB, BK, STAGES>() > 160 * 1024) {
+    if constexpr (lds_bytes<BM, BN, 64 * WAVES_M * WAVES_N, OB, BK, STAGES, I8>() > 160 * 1024) {
         return fhip::set_error(ctx, FHIP_ERR_UNSUPPORTED, "fp8 gemm: output tile too large for LDS");
     } else if constexpr (I8) {
         FHIP_GEMM_LAUNCH(OB, kScaleGeneral);

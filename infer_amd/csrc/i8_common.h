@@ -41,6 +41,29 @@ __device__ __forceinline__ int8_t requant_i8(double real, double s_out, double r
     return q;
 }
 
+// Requantization of an exact integer sum v (|v| < 2^24) with a per-column factor K = s_a * s_w / s_out held as
+// an unevaluated float pair kh + kl (K to ~2^-48): the code is clamp(round_half_away(v * K) + zp).  p = v * kh
+// and its exact rounding error e (one fma) give v * K = p + c, c = e + v * kl, to ~2^-45 |p|; with f = p - floor(p)
+// (exact for |p| < 2^23), d = (f - 0.5) + c has the sign of (v * K) - (floor(p) + 0.5) wherever |d| exceeds
+// 2^-36 (|p| + 1), and then the code is floor(p) + (d > 0) + zp, which is the reference's value (adding the
+// integer zp moves no x.5 point, and the reference's fp64 evaluation is within ~2^-50 of the exact value).
+// Otherwise (an x.5 point or closer than that, or |v| >= 2^24) `unsafe` is set and the caller decides with
+// the reference's arithmetic.  Magnitudes |p| >= 2^23 only ever clamp.
+__device__ __forceinline__ int8_t requant_i8_split(int32_t v, float kh, float kl, int32_t zp, bool& unsafe) {
+#pragma clang fp contract(off)
+    const float vf = (float)v;
+    const float p = vf * kh;
+    const float e = __builtin_fmaf(vf, kh, -p);
+    const float c = e + vf * kl;
+    const float fl = floorf(p);
+    const float d = ((p - fl) - 0.5f) + c;
+    unsafe = !(fabsf(d) > 0x1p-36f * (fabsf(p) + 1.0f)) || (uint32_t)(v + (1 << 24)) >= (2u << 24);
+    const float r = fl + (d > 0.0f ? 1.0f : 0.0f) + (float)zp;
+    const float hi = r < 127.0f ? r : 127.0f;
+    const float lo = hi > -128.0f ? hi : -128.0f;
+    return (int8_t)(int)lo;
+}
+
 struct I8Epilogue {
     int kind;
     const float* w_scales;   // [n] (per-tensor weights: all equal)
@@ -61,6 +84,17 @@ struct I8Epilogue {
     float dq_scale = 1.0f;
     int32_t dq_zp = 0;
     void* out_any = nullptr;
+    // Integer path (requant_i8_split): the sums' requantized value is (dot + bias) * K with K per column,
+    // i.e. MatMul, FC, or Gemm with alpha = beta = 1, and dot + bias provably inside int32 (host-set).
+    bool int_path = false;
+
+    // K = s_a * s_w / s_out of a column as the float pair kh + kl (fp64 product, as the reference's scale).
+    __device__ __forceinline__ void split_scale(float w_scale, float& kh, float& kl) const {
+#pragma clang fp contract(off)
+        const double kd = (double)s_a * (double)w_scale * recip_out;
+        kh = (float)kd;
+        kl = (float)(kd - (double)kh);
+    }
 
     // Per-output-channel parameters, loadable ahead of the main loop.
     struct Col {
@@ -76,20 +110,22 @@ struct I8Epilogue {
         store(raw, row, col, col_params(col));
     }
 
-    // The requantized INT8 code of the integer sum `raw` at (row, col).
-    __device__ __forceinline__ int8_t code(int32_t raw, int64_t row, int64_t col, const Col& c) const {
+    // The real value of the integer sum `raw` at (row, col) before requantization.
+    __device__ __forceinline__ double real(int32_t raw, int64_t row, int64_t col, const Col& c) const {
 #pragma clang fp contract(off)
         const int32_t dot = raw - zp_a * c.wsum;
         const int32_t b = bias_kind == FHIP_BIAS_MATRIX ? bias[row * ldo + col] : c.bias;
         const double scale = (double)s_a * (double)c.w_scale;
-        double real;
         if (kind == FHIP_I8_GEMM) {
             const double acc = alpha * (double)dot + beta * (double)b;
-            real = acc * scale;
-        } else {
-            real = (double)(dot + b) * scale;  // MatMul has no bias (b = 0)
+            return acc * scale;
         }
-        return requant_i8(real, inv_out_den, recip_out, zp_out);
+        return (double)(dot + b) * scale;  // MatMul has no bias (b = 0)
+    }
+
+    // The requantized INT8 code of the integer sum `raw` at (row, col).
+    __device__ __forceinline__ int8_t code(int32_t raw, int64_t row, int64_t col, const Col& c) const {
+        return requant_i8(real(raw, row, col, c), inv_out_den, recip_out, zp_out);
     }
 
     // DequantizeLinear of a code (fused output dtypes), quantize_linear_utils.h:291-341.

@@ -38,8 +38,13 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 // NW partial tiles are summed through LDS; integer sums are exact in any order.
 // MFMA depth 64: lane l supplies row/col l%16 and bytes [16*(l/16), 16*(l/16)+16) of the step.
 constexpr int kI8Unroll = 4;
-// From this many activation rows on, fhip_i8_linear runs the tile GEMM (i8_gemm_tile.hip) instead.
-constexpr int64_t kI8TileMinRows = 256;
+// fhip_i8_linear runs the tile GEMM (i8_gemm_tile.hip) from kI8TileMinRows activation rows on, and from
+// kI8TileMinRowsLarge rows when the product holds at least kI8TileMinMacs multiply-adds (measured crossovers:
+// the K-split kernel wins below ~384 rows at 1024 x 1024, below ~150 at 4096 x 4096, above 64 nowhere at
+// 3584 x 18944).
+constexpr int64_t kI8TileMinRows = 384;
+constexpr int64_t kI8TileMinRowsLarge = 64;
+constexpr double kI8TileMinMacs = 2.5e9;
 
 template <int FM, int FN, int NW = 4, int UNR = kI8Unroll>
 __global__ __launch_bounds__(NW * 64) void i8_gemm_kernel(const int8_t* __restrict__ a, int64_t m, int64_t k,
@@ -793,8 +798,12 @@ int fhip_i8_linear_ex(fhip_context ctx, int kind, const int8_t* a, float s_a, in
     ep.dq_scale = dq_scale;
     ep.dq_zp = dq_zp;
     ep.out_any = out;
+    ep.int_path = kind != FHIP_I8_GEMM ||
+                  (alpha == 1.0f && beta == 1.0f && int32_safe(w->k, zp_a, w->max_abs_w, babs));
     // Large M: the LDS-staged MFMA tile GEMM (operand reuse across a 128x128 or 256x256 tile).
-    if (m >= kI8TileMinRows && w->k % 64 == 0 && (reinterpret_cast<uintptr_t>(a) & 15) == 0 &&
+    const bool tile_rows =
+        m >= kI8TileMinRows || (m >= kI8TileMinRowsLarge && (double)m * (double)w->n * (double)w->k >= kI8TileMinMacs);
+    if (tile_rows && w->k % 64 == 0 && (reinterpret_cast<uintptr_t>(a) & 15) == 0 &&
         m * w->k < (int64_t(1) << 31))
         return fhip::launch_i8_gemm_tile(ctx, a, m, w, ep);
     const int64_t kp = ((w->k + 127) / 128) * 128;

@@ -22,10 +22,10 @@ def dev(a):
 CASES = [
     # m, k, n, kind, bias_kind, zp_a, zp_y, alpha, beta, pow2 scales, backend
     (512, 1024, 1024, po.I8_GEMM, po.BIAS_VECTOR, 0, 0, 1.0, 1.0, False, "i8_mfma_gemm_128x128_bk128_w8"),
-    (300, 192, 700, po.I8_GEMM, po.BIAS_MATRIX, -20, 10, 0.75, -1.5, True, "i8_mfma_gemm_128x128_w8"),
+    (420, 192, 700, po.I8_GEMM, po.BIAS_MATRIX, -20, 10, 0.75, -1.5, True, "i8_mfma_gemm_128x128_w8"),
     (3000, 256, 4000, po.I8_GEMM, po.BIAS_VECTOR, 7, -4, 1.0, 1.0, False, "i8_mfma_gemm_256x256_bk128_w8"),
     (3100, 320, 3900, po.I8_FC, po.BIAS_VECTOR, -3, 2, 1.0, 1.0, True, "i8_mfma_gemm_256x256_w8"),
-    (257, 128, 33, po.I8_MATMUL, po.BIAS_NONE, 12, 0, 1.0, 1.0, False, "i8_mfma_gemm_128x128_bk128_w8"),
+    (385, 128, 33, po.I8_MATMUL, po.BIAS_NONE, 12, 0, 1.0, 1.0, False, "i8_mfma_gemm_128x128_bk128_w8"),
     (777, 64, 515, po.I8_GEMM, po.BIAS_NONE, 0, -1, 2.0, 0.0, True, "i8_mfma_gemm_128x128_w8"),
 ]
 
