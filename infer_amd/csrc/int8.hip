@@ -27,6 +27,7 @@ using fhip::I8Epilogue;
 using fhip::clamp_round_i8;
 using fhip::requant_i8;
 using fhip::requant_i8_fast;
+using fhip::requant_i8_split;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -597,20 +598,27 @@ __global__ __launch_bounds__(256) void i8_conv_window_kernel(const int8_t* __res
         }
     }
     // C fragment of lane l: channel l%16, pixels 4*(l/16) .. +3 (consecutive output x).
-    // Requantize every value on the reciprocal path first; values near an x.5 point are redone with the
-    // division in one cold branch (rare), so the hot tail holds no per-value branch.
+    // Requantize every value on the integer path (requant_i8_split: acc + shift is the exact int32 sum,
+    // K = s_in * s_w / s_out a float pair per channel); values it cannot decide (x.5 points) are redone
+    // with the reference's fp64 division in one cold branch, so the hot tail holds no per-value branch.
     int8_t qv[kConvFrags][WNF][4];
     uint32_t ties = 0;
+    float kh[WNF], kl[WNF];
+    int32_t shift[WNF];
+#pragma unroll
+    for (int j = 0; j < WNF; ++j) {
+        ep.split_scale(e_scale[j], kh[j], kl[j]);
+        shift[j] = e_bias[j] - (int32_t)g.zp_in * e_wsum[j];
+    }
+    const int32_t zp_out_i = (int32_t)ep.zp_out;
 #pragma unroll
     for (int f = 0; f < kConvFrags; ++f)
 #pragma unroll
         for (int j = 0; j < WNF; ++j) {
-            const double scale = (double)ep.s_a * (double)e_scale[j];
-            const int32_t shift = e_bias[j] - (int32_t)g.zp_in * e_wsum[j];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 bool tie;
-                qv[f][j][r] = requant_i8_fast((double)(acc[f][j][r] + shift) * scale, ep.recip_out, ep.zp_out, tie);
+                qv[f][j][r] = requant_i8_split(acc[f][j][r] + shift[j], kh[j], kl[j], zp_out_i, tie);
                 ties |= (uint32_t)tie << ((f * WNF + j) * 4 + r);
             }
         }

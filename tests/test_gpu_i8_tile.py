@@ -106,3 +106,30 @@ def test_i8_tile_gemm_unaligned_activation_uses_small_tiles(ctx):
     assert ctx.last_backend().endswith("_ksplit4")
     assert np.array_equal(out.cpu().numpy(), ref)
     wt.release()
+
+
+def test_i8_tile_gemm_sums_beyond_2_24(ctx):
+    """Sums of magnitude above 2^24 (not exact in fp32: the integer path hands them to the fp64 pass) with an
+    output scale that keeps most codes unclamped, next to small sums in the same tile."""
+    r = rng(91)
+    m, k, n = 512, 4096, 256
+    sign_a = r.choice([-1, 1], (m, 1))
+    sign_w = r.choice([-1, 1], (n, 1))
+    xq = (sign_a * r.integers(100, 128, (m, k))).astype(np.int8)
+    xq[::7] = r.integers(-128, 128, (len(xq[::7]), k)).astype(np.int8)  # small sums in every tile
+    w = (sign_w * r.integers(100, 128, (n, k))).astype(np.int8)
+    w_kn = np.ascontiguousarray(w.T)  # FC weights are [K, N]
+    s_w = r.uniform(9e-4, 1.1e-3, n).astype(np.float32)
+    s_x, s_y = 0.01, 6.45
+    for zp_y in (0, -37):
+        rc, ref, _ = po.i8_linear(po.I8_FC, xq, s_x, 0, w_kn, False, s_w, None, None, po.BIAS_NONE, 1.0, 1.0, s_y,
+                                  zp_y)
+        assert rc == 0
+        assert np.count_nonzero(np.abs(ref.astype(int) - zp_y) < 100) > ref.size // 4
+        wt = ctx.prepare_weight(dev(w_kn), po.INT8, k, n, 0, scales=s_w, version=600)
+        out = torch.empty((m, n), dtype=torch.int8, device="cuda")
+        ctx.i8_linear(po.I8_FC, dev(xq), s_x, 0, m, wt, out, s_y, zp_y)
+        assert ctx.last_backend().startswith("i8_mfma_gemm_")
+        got = out.cpu().numpy()
+        assert np.array_equal(got, ref), f"zp_y={zp_y}: {np.count_nonzero(got != ref)} mismatches"
+        wt.release()
