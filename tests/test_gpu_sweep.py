@@ -1,6 +1,8 @@
 """Seeded random sweeps over the entry points' shape space, against the oracle, to the same bars as the focused
 tests: INT8 Conv2D bit-exact over groups (window, gathered and one-channel-per-group kernels), both layouts,
-strides, padding, dilation and zero points; FP8 linear within one code or the fp32 summation-order bound;
+strides, padding, dilation and zero points; INT8 MatMul/FC/Gemm bit-exact over M (both the K-split and the
+tile kernels), K, N, zero points, bias kinds, alpha/beta and fused DequantizeLinear outputs; FP8 linear within
+one code or the fp32 summation-order bound;
 BF16 argmax tokens exact up to the order-induced BF16 boundary flip rule."""
 import numpy as np
 import pytest
@@ -60,6 +62,53 @@ def test_sweep_i8_conv(ctx, seed):
     got = out.cpu().numpy()
     print(p, ctx.last_backend())
     assert np.array_equal(got, ref), f"{p} ({ctx.last_backend()}): {np.count_nonzero(got != ref)} mismatches"
+    wt.release()
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_sweep_i8_linear(ctx, seed):
+    r = rng(6000 + seed)
+    kind = int(r.choice([po.I8_GEMM, po.I8_FC, po.I8_MATMUL]))
+    m = int(r.choice([1, 7, 16, 33, 100, 200, 385, 512, 700, 1100]))
+    k = int(r.choice([16, 48, 64, 128, 320, 1024, 2048]))
+    n = int(r.integers(1, 900))
+    zp_a, zp_y = int(r.integers(-30, 31)), int(r.integers(-20, 21))
+    bias_kind = po.BIAS_NONE if kind == po.I8_MATMUL else int(r.choice([po.BIAS_NONE, po.BIAS_VECTOR, po.BIAS_MATRIX]))
+    if kind == po.I8_FC and bias_kind == po.BIAS_MATRIX:
+        bias_kind = po.BIAS_VECTOR
+    alpha, beta = (1.0, 1.0) if kind != po.I8_GEMM or r.random() < 0.6 else (float(r.choice([0.5, 0.75, 2.0])),
+                                                                             float(r.choice([-1.5, 0.0, 1.0])))
+    pow2 = r.random() < 0.3
+    out_dtype = int(r.choice([po.INT8, po.INT8, po.FP32, po.FP16, po.BF16]))
+    xq = r.integers(-128, 128, (m, k)).astype(np.int8)
+    w = r.integers(-127, 128, (n, k)).astype(np.int8)
+    s_w = np.full(n, 2.0 ** -8, np.float32) if pow2 else r.uniform(1e-3, 1e-2, n).astype(np.float32)
+    s_x, s_y = (0.0625, 2.0) if pow2 else (0.02, float(r.uniform(0.05, 0.5)))
+    bias = None
+    if bias_kind == po.BIAS_VECTOR:
+        bias = r.integers(-20000, 20000, n).astype(np.int32)
+    elif bias_kind == po.BIAS_MATRIX:
+        bias = r.integers(-3000, 3000, (m, n)).astype(np.int32)
+    trans_b = kind == po.I8_GEMM
+    w_src = w if trans_b else np.ascontiguousarray(w.T)
+    rc, ref, _ = po.i8_linear(kind, xq, s_x, zp_a, w_src, trans_b, s_w, None, bias, bias_kind, alpha, beta, s_y, zp_y)
+    assert rc == 0
+    s_dq, zp_dq = 0.0125, 3
+    if out_dtype != po.INT8:
+        rc, ref = po.dequantize_linear(ref, [s_dq], [zp_dq], out_dtype)
+        assert rc == 0
+    wt = ctx.prepare_weight(dev(w_src), po.INT8, k, n, 1 if trans_b else 0, scales=s_w, version=700 + seed)
+    tdt = {po.INT8: torch.int8, po.FP32: torch.float32}.get(out_dtype, torch.int16)
+    out = torch.empty((m, n), dtype=tdt, device="cuda")
+    kw = {}
+    if bias is not None:
+        kw = dict(bias=dev(bias), bias_kind=bias_kind, bias_abs_max=int(np.abs(bias).max()))
+    ctx.i8_linear_ex(kind, dev(xq), s_x, zp_a, m, wt, out, out_dtype, s_y, zp_y, dq_scale=s_dq, dq_zp=zp_dq,
+                     alpha=alpha, beta=beta, **kw)
+    got = out.cpu().numpy()
+    case = f"kind={kind} m={m} k={k} n={n} bias={bias_kind} ab=({alpha},{beta}) out={out_dtype} ({ctx.last_backend()})"
+    print(case)
+    assert np.array_equal(got.view(np.uint8), np.ascontiguousarray(ref).view(np.uint8)), case
     wt.release()
 
 
