@@ -34,6 +34,9 @@ namespace {
 
 using namespace fhip;
 
+// The FP8 instantiations take this empty stand-in, so their kernel arguments stay as small as before.
+struct NoI8Epilogue {};
+
 typedef int v16i_t __attribute__((ext_vector_type(16)));
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 
@@ -216,7 +219,7 @@ template <bool E5, int BM, int BN, int WAVES_M, int WAVES_N, int OUT_BYTES, int 
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const uint8_t* __restrict__ a, int64_t m, int64_t k,
                                                        const uint8_t* __restrict__ b, int64_t kp, int64_t np,
                                                        int tiles_n, int tiles_total, XcdMap xm, int mfma_scale, Fp8Epilogue ep,
-                                                       I8Epilogue iep) {
+                                                       std::conditional_t<I8, I8Epilogue, NoI8Epilogue> iep) {
     constexpr int NT = 64 * WAVES_M * WAVES_N;
     using S = Stage<BM, BN, NT, BK>;
     constexpr int kSub = BK / 64;  // 64-deep MFMA steps per stage
@@ -658,10 +661,12 @@ int launch_tile(fhip_context ctx, const uint8_t* a, int64_t m, int64_t k64, cons
             mfma_scale = 127 + (e - 1);
         }
     }
+    std::conditional_t<I8, I8Epilogue, NoI8Epilogue> i8_arg{};
+    if constexpr (I8) i8_arg = *iep;
 #define FHIP_GEMM_LAUNCH(OB, SMV)                                                                                   \
     fp8_gemm_kernel<E5, BM, BN, WAVES_M, WAVES_N, OB, SMV, BK, STAGES, WTN1, I8><<<grid, 64 * WAVES_M * WAVES_N,                       \
                                                           lds_bytes<BM, BN, 64 * WAVES_M * WAVES_N, OB, BK, STAGES, I8>(), ctx->stream>>>( \
-        a, m, k64, wd, kp, np, tiles_n, tiles, xm, mfma_scale, ep, iep ? *iep : I8Epilogue{})
+        a, m, k64, wd, kp, np, tiles_n, tiles, xm, mfma_scale, ep, i8_arg)
 #define FHIP_GEMM_LAUNCH_SM(OB)                                                                                     \
     do {                                                                                                            \
         if (sm == kScaleFolded) FHIP_GEMM_LAUNCH(OB, kScaleFolded);                                                 \
