@@ -54,7 +54,7 @@ def parse():
                    help="headline only, graph-replayed launches only (no eager event pairs or dispatch reference "
                         "points): the run rocprofv3 traces for the headline kernel's per-dispatch duration")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--configs", default="", help="comma list of extra configs to run (C1..C5; default all)")
+    p.add_argument("--configs", default="", help="comma list of extra configs to run (C1..C5; default all; I8L: opt-in INT8 linear at larger M)")
     return p.parse_args()
 
 
@@ -553,6 +553,27 @@ def extra_configs(b, args):
             by = v * k * 2 + m * k * 2 + m * 8
             res[f"C5_bf16_argmax_M{m}"] = {"ms_per_step": ms, "GB/s": by / ms / 1e6, "hbm_frac": by / ms / 1e6 / HBM_PEAK_GBS,
                                            "kernel_ms_event_pairs": km}
+
+    if chosen is not None and "I8L" in chosen:
+        # Opt-in (not a BASELINE config): the INT8 linear at larger M, where fhip_i8_linear runs the MFMA tile
+        # GEMM; FC, per-channel weight scales, INT8 output.  Operands stay resident (MFMA-bound shapes).
+        INT8_PEAK_TOPS = 5000.0
+        for m, k, n in ((4096, 4096, 4096), (4096, 18944, 3584), (1024, 4096, 4096), (4096, 1024, 3584)):
+            b.gen.manual_seed(0xFEA7000A + m + k + n)
+            a8 = t.randint(-128, 128, (m, k), generator=b.gen, device="cuda", dtype=t.int8)
+            w8 = t.randint(-127, 128, (n, k), generator=b.gen, device="cuda", dtype=t.int8)
+            s_w = (t.rand(n, generator=b.gen, device="cuda") * 9e-3 + 1e-3).cpu().numpy()
+            wp = ctx.prepare_weight(w8, L.INT8, k, n, L.LAYOUT_NK, scales=s_w, version=10)
+            o8 = t.empty((m, n), dtype=t.int8, device="cuda")
+
+            def i8l(i=0, a8=a8, wp=wp, o8=o8, m=m):
+                ctx.i8_linear(L.I8_FC, a8, 0.01, 0, m, wp, o8, 0.5, 0)
+            ms, _ = b.graph_time([i8l] * 10, 5)
+            tops = 2.0 * m * n * k / ms / 1e9
+            res[f"I8L_int8_fc_{m}x{k}x{n}"] = {"ms_per_step": ms, "TOPS": tops, "mfma_frac": tops / INT8_PEAK_TOPS,
+                                               "backend": ctx.last_backend()}
+            wp.release()
+            del a8, w8, o8
 
     return res
 

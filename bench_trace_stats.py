@@ -4,7 +4,9 @@ profiles quote its output.
     python bench_trace_stats.py <dir>/**/<name>_kernel_trace.csv [--match REGEX] [--tail N]
         duration per dispatch: calls, average, median, minimum, maximum (ns);
         --tail N keeps only each kernel's last N dispatches (for bench.py --trace-headline, whose last
-        launches are the timed graph replays)
+        launches are the timed graph replays);
+        --runs: one row per run of consecutive matching dispatches of one kernel and grid size (a bench
+        config that times several shapes of one kernel one after the other)
     python bench_trace_stats.py --counters <dir>/**/<name>_counter_collection.csv [--match REGEX]
         median value per dispatch of every counter (a kernel's dispatches summed per dispatch id)
 """
@@ -21,6 +23,7 @@ def main():
     p.add_argument("trace", help="kernel_trace.csv path or glob")
     p.add_argument("--match", default="", help="only kernels whose name matches this regex")
     p.add_argument("--tail", type=int, default=0)
+    p.add_argument("--runs", action="store_true")
     p.add_argument("--counters", action="store_true", help="the file is a counter_collection.csv")
     args = p.parse_args()
     if args.counters:
@@ -32,10 +35,13 @@ def main():
     for path in paths:
         with open(path, newline="") as f:
             for r in csv.DictReader(f):
-                rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+                rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"],
+                             r.get("Grid_Size_X", "")))
     rows.sort()
+    if args.runs:
+        return runs(args, rows)
     per = {}
-    for s, e, name in rows:
+    for s, e, name, _ in rows:
         if args.match and not re.search(args.match, name):
             continue
         per.setdefault(name, []).append(e - s)
@@ -46,6 +52,22 @@ def main():
             d = d[-args.tail:]
         print(f"| `{name[:110]}` | {len(d)} | {statistics.mean(d):.0f} | {statistics.median(d):.0f} | {min(d)} | "
               f"{max(d)} |")
+
+
+def runs(args, rows):
+    out = []  # [(name, grid, durations)]
+    for s, e, name, grid in rows:
+        if args.match and not re.search(args.match, name):
+            continue
+        if out and out[-1][0] == name and out[-1][1] == grid:
+            out[-1][2].append(e - s)
+        else:
+            out.append((name, grid, [e - s]))
+    print("| kernel | grid | calls | avg ns | median ns | min ns | max ns |")
+    print("|---|---|---|---|---|---|---|")
+    for name, grid, d in out:
+        print(f"| `{name[:110]}` | {grid} | {len(d)} | {statistics.mean(d):.0f} | {statistics.median(d):.0f} | "
+              f"{min(d)} | {max(d)} |")
 
 
 def counters(args):
