@@ -350,19 +350,25 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
     int scale_v;
     asm volatile("v_mov_b32 %0, %1" : "=v"(scale_v) : "s"(mfma_scale));
     auto mfmas = [&](const u32x4_t (&fa)[FM][2], const u32x4_t (&fb)[FN][2]) {
+        if constexpr (I8) {
+            // Two MFMAs per 64-deep step, one per 16-byte half of each lane's K slice.  The half is the outer
+            // loop so consecutive MFMAs write different accumulators (no back-to-back dependency).  Weight
+            // fragment as the row operand: each 32x32 block is computed transposed.
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                if constexpr (I8) {
-                    // weight fragment as the row operand: each 32x32 block is computed transposed
+                for (int i = 0; i < FM; ++i)
 #pragma unroll
-                    for (int h = 0; h < 2; ++h) {
+                    for (int j = 0; j < FN; ++j) {
                         const v4i_t av = v4i_t{(int)fa[i][h].x, (int)fa[i][h].y, (int)fa[i][h].z, (int)fa[i][h].w};
                         const v4i_t bv = v4i_t{(int)fb[j][h].x, (int)fb[j][h].y, (int)fb[j][h].z, (int)fb[j][h].w};
                         acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bv, av, acc[i][j], 0, 0, 0);
                     }
-                } else {
+        } else {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
                     const v8i av = v8i{(int)fa[i][0].x, (int)fa[i][0].y, (int)fa[i][0].z, (int)fa[i][0].w,
                                        (int)fa[i][1].x, (int)fa[i][1].y, (int)fa[i][1].z, (int)fa[i][1].w};
                     const v8i bv = v8i{(int)fb[j][0].x, (int)fb[j][0].y, (int)fb[j][0].z, (int)fb[j][0].w,
@@ -370,7 +376,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
                     // weight fragment as the row operand: each 32x32 block is computed transposed
                     acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[i][j], fmt, fmt, 0, scale_v, 0, 127);
                 }
-            }
+        }
         // Pin the MFMAs here: they are pure operations, which IR-level code motion may sink below the
         // following lgkmcnt fence (sched_barrier binds only the machine scheduler).  Volatile asm keeps
         // its order with the fence.
@@ -500,100 +506,113 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
         }
     };
     if constexpr (I8) {
-        // INT8: each value's requantized code (I8Epilogue: zero-point correction, bias, alpha/beta, scales),
-        // then the code itself (OUT_BYTES 1) or its DequantizeLinear value (2: FP16/BF16, 4: FP32).  The hot
-        // pass decides every code in fp32 (requant_i8_f32's error bound) and flags, one bit per value, those
-        // it cannot decide (near an x.5 point).  Positions past m or n are never stored and not evaluated, so
-        // a bias is read only inside the output.
-        constexpr int kElems = FM * FN * 16;
-        uint32_t unsafe_bits[(kElems + 31) / 32] = {};
-        uint32_t any_unsafe = 0;
+        // INT8: the int32 accumulators go through LDS one fragment row at a time (a slab of WAVES_M x 32 rows
+        // by BN columns), and a rolled loop requantizes four consecutive values per thread (I8Epilogue:
+        // zero-point correction, bias, alpha/beta, scales) and stores their codes (OUT_BYTES 1) or their
+        // DequantizeLinear values (2: FP16/BF16, 4: FP32) straight to the output.  Unrolled over the 64 to
+        // 128 accumulators of a lane, the same work held the whole accumulator set live through a long
+        // branchy tail and spilled.  The integer path decides each code with requant_i8_split; values it
+        // cannot decide (x.5 points) take the reference's fp64 arithmetic in place.
+        static_assert(WTN1 == 0, "INT8 mode: equal wave columns");
+        constexpr int kSlabRows = WAVES_M * 32;
+        constexpr int kChunksRow = BN / 4;  // 16-byte chunks of int32 per staged row
+        static_assert((size_t)kSlabRows * BN * 4 <= kColOff, "INT8 slab must not reach the column parameters");
+        int32_t* const slab = reinterpret_cast<int32_t*>(smem);
+        // chunk swizzle: the 32 rows of one ds_write_b128 group land on distinct 16-byte bank groups
+        auto slab_at = [&](int srow, int chunk) __attribute__((always_inline)) {
+            return slab + srow * BN + ((chunk ^ ((srow & (kChunksRow / 2 - 1)) << 1)) << 2);
+        };
+        const int rows_in = (int)(m - m0 < BM ? m - m0 : BM);
+        const int cols_in = (int)(iep.ldo - n0 < BN ? iep.ldo - n0 : BN);
         const int32_t zp_out_i = (int32_t)iep.zp_out;
-        auto hot = [&](auto int_tag) __attribute__((always_inline)) {
-            constexpr bool INT = decltype(int_tag)::value;
-            static_for<FM * FN>([&](auto ij) {
-                constexpr int i = decltype(ij)::value / FN, j = decltype(ij)::value % FN;
+        const int32_t* colp = reinterpret_cast<const int32_t*>(smem + kColOff);
+        static_for<FM>([&](auto ii) {
+            constexpr int i = decltype(ii)::value;
+            if (i > 0) __syncthreads();  // the previous slab has been read
+            static_for<FN>([&](auto jj) {
+                constexpr int j = decltype(jj)::value;
                 static_for<4>([&](auto gg) {
                     constexpr int g = decltype(gg)::value;
-                    constexpr int e0 = (decltype(ij)::value * 4 + g) * 4;
-                    const int r = wm * WTM + i * 32 + row_in;
                     const int c = wcol + j * 32 + g * 8 + col_q;
-                    const int64_t row = m0 + r, col = n0 + c;
-                    const uint8_t* cp = smem + kColOff + c * 4;
-                    const int4 p0 = *reinterpret_cast<const int4*>(cp);
-                    const int4 p1 = *reinterpret_cast<const int4*>(cp + BN * 4);
-                    const float4 p2 = *reinterpret_cast<const float4*>(cp + BN * 8);
-                    const int a0[4] = {p0.x, p0.y, p0.z, p0.w}, a1[4] = {p1.x, p1.y, p1.z, p1.w};
-                    const float a2[4] = {p2.x, p2.y, p2.z, p2.w};
-                    int8_t q[4];
+                    *reinterpret_cast<int4*>(slab_at(wm * 32 + row_in, c >> 2)) =
+                        make_int4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+                });
+            });
+            __syncthreads();
+            for (int q = tid; q < kSlabRows * kChunksRow; q += NT) {
+                const int srow = q / kChunksRow, chunk = q % kChunksRow;
+                const int r = (srow >> 5) * WTM + i * 32 + (srow & 31);
+                const int c = chunk * 4;
+                if (r >= rows_in || c >= cols_in) continue;
+                const int4 raw4 = *reinterpret_cast<const int4*>(slab_at(srow, chunk));
+                const int raw[4] = {raw4.x, raw4.y, raw4.z, raw4.w};
+                const int4 p0 = *reinterpret_cast<const int4*>(colp + c);
+                const int4 p1 = *reinterpret_cast<const int4*>(colp + BN + c);
+                const int4 p2 = *reinterpret_cast<const int4*>(colp + 2 * BN + c);
+                const int a0[4] = {p0.x, p0.y, p0.z, p0.w}, a1[4] = {p1.x, p1.y, p1.z, p1.w};
+                const int a2[4] = {p2.x, p2.y, p2.z, p2.w};
+                const int64_t row = m0 + r, col = n0 + c;
+                const int nv = cols_in - c < 4 ? cols_in - c : 4;
+                int8_t qv[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    bool unsafe;
+                    if (iep.int_path) {
+                        // a0 = shift (bias - zp_a * wsum), a1 = kl bits, a2 = kh bits
+                        int32_t v = raw[t] + a0[t];
+                        if (iep.bias_kind == FHIP_BIAS_MATRIX) v += iep.bias[row * iep.ldo + col + (t < nv ? t : 0)];
+                        qv[t] = requant_i8_split(v, __int_as_float(a2[t]), __int_as_float(a1[t]), zp_out_i, unsafe);
+                    } else {
+                        const I8Epilogue::Col cpt{a0[t], a1[t], __int_as_float(a2[t])};
+                        const int64_t ct = col + (t < nv ? t : 0);
+                        qv[t] = requant_i8_fast(iep.real(raw[t], row, ct, cpt), iep.recip_out, iep.zp_out, unsafe);
+                    }
+                    if (__builtin_expect(unsafe && t < nv, 0))
+                        qv[t] = iep.code(raw[t], row, col + t, iep.col_params(col + t));
+                }
+                const int64_t idx = row * iep.ldo + col;
+                if constexpr (OUT_BYTES == 1) {
+                    int8_t* dst = static_cast<int8_t*>(iep.out_any) + idx;
+                    if (nv == 4 && (reinterpret_cast<uintptr_t>(dst) & 3) == 0) {
+                        *reinterpret_cast<uint32_t*>(dst) = (uint32_t)(uint8_t)qv[0] | (uint32_t)(uint8_t)qv[1] << 8 |
+                                                            (uint32_t)(uint8_t)qv[2] << 16 |
+                                                            (uint32_t)(uint8_t)qv[3] << 24;
+                    } else {
+#pragma unroll
+                        for (int t = 0; t < 4; ++t)
+                            if (t < nv) dst[t] = qv[t];
+                    }
+                } else if constexpr (OUT_BYTES == 2) {
+                    uint16_t h[4];
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
-                        q[t] = 0;
-                        if (row < m && col + t < iep.ldo) {
-                            bool unsafe;
-                            if constexpr (INT) {
-                                // a0 = shift, a1 = kl bits, a2 = kh
-                                int32_t v = acc[i][j][4 * g + t] + a0[t];
-                                if (iep.bias_kind == FHIP_BIAS_MATRIX) v += iep.bias[row * iep.ldo + col + t];
-                                q[t] = requant_i8_split(v, a2[t], __int_as_float(a1[t]), zp_out_i, unsafe);
-                            } else {
-                                const I8Epilogue::Col cpt{a0[t], a1[t], a2[t]};
-                                const double v = iep.real(acc[i][j][4 * g + t], row, col + t, cpt);
-                                q[t] = requant_i8_fast(v, iep.recip_out, iep.zp_out, unsafe);
-                            }
-                            unsafe_bits[(e0 + t) / 32] |= (uint32_t)unsafe << ((e0 + t) % 32);
-                            any_unsafe |= (uint32_t)unsafe;
-                        }
+                        const float v = iep.dequant(qv[t]);
+                        h[t] = iep.out_dtype == FHIP_FP16 ? fhip::fp16_encode(v) : fhip::bf16_encode_plain(v);
                     }
-                    uint8_t* dst = so + r * kOutPitch + c * OUT_BYTES;
-                    if constexpr (OUT_BYTES == 1) {
-                        *reinterpret_cast<uint32_t*>(dst) = (uint32_t)(uint8_t)q[0] | (uint32_t)(uint8_t)q[1] << 8 |
-                                                            (uint32_t)(uint8_t)q[2] << 16 | (uint32_t)(uint8_t)q[3] << 24;
-                    } else if constexpr (OUT_BYTES == 2) {
-                        uint16_t h[4];
-#pragma unroll
-                        for (int t = 0; t < 4; ++t) {
-                            const float v = iep.dequant(q[t]);
-                            h[t] = iep.out_dtype == FHIP_FP16 ? fhip::fp16_encode(v) : fhip::bf16_encode_plain(v);
-                        }
+                    uint16_t* dst = static_cast<uint16_t*>(iep.out_any) + idx;
+                    if (nv == 4 && (reinterpret_cast<uintptr_t>(dst) & 7) == 0) {
                         *reinterpret_cast<uint2*>(dst) = make_uint2((uint32_t)h[0] | (uint32_t)h[1] << 16,
                                                                     (uint32_t)h[2] | (uint32_t)h[3] << 16);
                     } else {
-                        *reinterpret_cast<float4*>(dst) =
-                            make_float4(iep.dequant(q[0]), iep.dequant(q[1]), iep.dequant(q[2]), iep.dequant(q[3]));
+#pragma unroll
+                        for (int t = 0; t < 4; ++t)
+                            if (t < nv) dst[t] = h[t];
                     }
-                });
-            });
-        };
-        if (iep.int_path) hot(std::true_type{});
-        else hot(std::false_type{});
-        // Cold pass: only the flagged values are recomputed with the reference's fp64 arithmetic (column
-        // parameters from global memory: the integer path rewrote the staged ones) and patched into the
-        // staged tile (same thread, same LDS bytes).
-        if (__builtin_expect(any_unsafe != 0, 0)) {
-            static_for<FM * FN>([&](auto ij) {
-                constexpr int i = decltype(ij)::value / FN, j = decltype(ij)::value % FN;
-                static_for<16>([&](auto ee) {
-                    constexpr int e = decltype(ee)::value, g = e / 4, t = e % 4;
-                    constexpr int bit = decltype(ij)::value * 16 + e;
-                    if (unsafe_bits[bit / 32] & (1u << (bit % 32))) {
-                        const int r = wm * WTM + i * 32 + row_in;
-                        const int c = wcol + j * 32 + g * 8 + col_q + t;
-                        const int8_t q = iep.code(acc[i][j][e], m0 + r, n0 + c, iep.col_params(n0 + c));
-                        uint8_t* dst = so + r * kOutPitch + c * OUT_BYTES;
-                        if constexpr (OUT_BYTES == 1) {
-                            *reinterpret_cast<int8_t*>(dst) = q;
-                        } else if constexpr (OUT_BYTES == 2) {
-                            const float v = iep.dequant(q);
-                            *reinterpret_cast<uint16_t*>(dst) =
-                                iep.out_dtype == FHIP_FP16 ? fhip::fp16_encode(v) : fhip::bf16_encode_plain(v);
-                        } else {
-                            *reinterpret_cast<float*>(dst) = iep.dequant(q);
-                        }
+                } else {
+                    float* dst = static_cast<float*>(iep.out_any) + idx;
+                    const float4 v = make_float4(iep.dequant(qv[0]), iep.dequant(qv[1]), iep.dequant(qv[2]),
+                                                 iep.dequant(qv[3]));
+                    if (nv == 4 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+                        *reinterpret_cast<float4*>(dst) = v;
+                    } else {
+                        const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                        for (int t = 0; t < 4; ++t)
+                            if (t < nv) dst[t] = vv[t];
                     }
-                });
-            });
-        }
+                }
+            }
+        });
     } else {
         if (ep.bias_kind != FHIP_BIAS_NONE) epilogue(std::true_type{});
         else epilogue(std::false_type{});
@@ -602,6 +621,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
     // wave-uniform branch; both bodies run the same sequence of barriers
     if (WTN1 == 0 || wn == 0) body(std::integral_constant<int, FN0>{});
     else body(std::integral_constant<int, (FN1 > 0 ? FN1 : 1)>{});
+    if constexpr (I8) return;  // the INT8 epilogue stored its values itself
     __syncthreads();
     constexpr int kChunks = BN * OUT_BYTES / 16;
     const int64_t n_bytes = ep.n * OUT_BYTES;
