@@ -22,6 +22,10 @@
 //     so the tile index is re-derived to give each XCD a rectangle of tiles whose shared operand rows
 //     fit in that XCD's L2 (XcdMap);
 //   * epilogue: accumulators -> output bits -> LDS tile -> coalesced 16-byte global stores.
+//
+// The same kernel in its INT8 mode (template flag I8; i8_gemm_tile.hip): int8 operands, two
+// v_mfma_i32_32x32x32_i8 per 64-deep step, int32 accumulators, and I8Epilogue's requantization (i8_common.h)
+// in a rolled loop over accumulators staged through LDS.
 #ifndef FHIP_FP8_GEMM_IMPL_H
 #define FHIP_FP8_GEMM_IMPL_H
 #include "fp8_common.h"
