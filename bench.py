@@ -557,7 +557,6 @@ def extra_configs(b, args):
     if chosen is not None and "I8L" in chosen:
         # Opt-in (not a BASELINE config): the INT8 linear at larger M, where fhip_i8_linear runs the MFMA tile
         # GEMM; FC, per-channel weight scales, INT8 output.  Operands stay resident (MFMA-bound shapes).
-        INT8_PEAK_TOPS = 5000.0
         for m, k, n in ((4096, 4096, 4096), (4096, 18944, 3584), (1024, 4096, 4096), (4096, 1024, 3584)):
             b.gen.manual_seed(0xFEA7000A + m + k + n)
             a8 = t.randint(-128, 128, (m, k), generator=b.gen, device="cuda", dtype=t.int8)
