@@ -529,6 +529,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
         const int rows_in = (int)(m - m0 < BM ? m - m0 : BM);
         const int cols_in = (int)(iep.ldo - n0 < BN ? iep.ldo - n0 : BN);
         const int32_t zp_out_i = (int32_t)iep.zp_out;
+        const float zp_half = (float)zp_out_i + 0.5f;
         const int32_t* colp = reinterpret_cast<const int32_t*>(smem + kColOff);
         static_for<FM>([&](auto ii) {
             constexpr int i = decltype(ii)::value;
@@ -562,10 +563,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
                 for (int t = 0; t < 4; ++t) {
                     bool unsafe;
                     if (iep.int_path) {
-                        // a0 = shift (bias - zp_a * wsum), a1 = kl bits, a2 = kh bits
+                        // a0 = shift (bias - zp_a * wsum), a1 = kl bits, a2 = kh bits; the cheap screen
+                        // first, the float-pair form where it cannot decide (about 2^-10 of the values)
                         int32_t v = raw[t] + a0[t];
                         if (iep.bias_kind == FHIP_BIAS_MATRIX) v += iep.bias[row * iep.ldo + col + (t < nv ? t : 0)];
-                        qv[t] = requant_i8_split(v, __int_as_float(a2[t]), __int_as_float(a1[t]), zp_out_i, unsafe);
+                        qv[t] = requant_i8_screen(v, __int_as_float(a2[t]), zp_half, unsafe);
+                        if (__builtin_expect(unsafe, 0))
+                            qv[t] = requant_i8_split(v, __int_as_float(a2[t]), __int_as_float(a1[t]), zp_out_i, unsafe);
                     } else {
                         const I8Epilogue::Col cpt{a0[t], a1[t], __int_as_float(a2[t])};
                         const int64_t ct = col + (t < nv ? t : 0);

@@ -64,6 +64,22 @@ __device__ __forceinline__ int8_t requant_i8_split(int32_t v, float kh, float kl
     return (int8_t)(int)lo;
 }
 
+// Cheaper screen for the same requantization, for loops that can afford a per-value second step: with
+// t = fl32(fl32(v) * kh) + (zp + 0.5) rounded once more, |t - (v*K + zp + 0.5)| <= 3.0000001 * 2^-24 |v*K| +
+// 2^-24 |t| < 2^-12 whenever |v*K| <= 1024 (fl32(v) may itself be rounded: |v| < 2^31).  So floor(t) is the
+// reference's code wherever t - floor(t) is at least 2^-11 from 0 and from 1; otherwise `unsafe` is set and the
+// caller decides with requant_i8_split (and the fp64 form).  Where |v*K| > 1024 the value lies beyond +-895
+// and both clamp to the same code.  About 2^-10 of uniformly spread values are flagged.
+__device__ __forceinline__ int8_t requant_i8_screen(int32_t v, float kh, float zp_half, bool& unsafe) {
+#pragma clang fp contract(off)
+    const float t = (float)v * kh + zp_half;
+    const float fl = floorf(t);
+    unsafe = fabsf((t - fl) - 0.5f) > 0.5f - 0x1p-11f;
+    const float hi = fl < 127.0f ? fl : 127.0f;
+    const float lo = hi > -128.0f ? hi : -128.0f;
+    return (int8_t)(int)lo;
+}
+
 struct I8Epilogue {
     int kind;
     const float* w_scales;   // [n] (per-tensor weights: all equal)
