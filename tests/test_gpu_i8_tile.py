@@ -133,3 +133,26 @@ def test_i8_tile_gemm_sums_beyond_2_24(ctx):
         got = out.cpu().numpy()
         assert np.array_equal(got, ref), f"zp_y={zp_y}: {np.count_nonzero(got != ref)} mismatches"
         wt.release()
+
+
+@pytest.mark.parametrize("m", [100, 512])
+def test_i8_linear_near_ties(ctx, m):
+    """s_a * s_w / s_out = 0.5 * (1 + 2^-22): every odd sum lands a few 1e-7 .. 1e-4 from an x.5 point, inside
+    the fp32 screen's margin but decided by the float-pair form (and exactly on x.5 for s_w = 1); both
+    kernels (K-split for m = 100, tile for m = 512)."""
+    r = rng(95 + m)
+    k, n = 64, 256
+    xq = r.integers(-2, 3, (m, k)).astype(np.int8)
+    w = r.integers(-2, 3, (n, k)).astype(np.int8)
+    s_w = np.where(np.arange(n) % 2 == 0, np.float32(1.0 + 2.0 ** -22), np.float32(1.0)).astype(np.float32)
+    w_kn = np.ascontiguousarray(w.T)
+    for zp_y in (0, 3, -7):
+        rc, ref, _ = po.i8_linear(po.I8_FC, xq, 0.5, 0, w_kn, False, s_w, None, None, po.BIAS_NONE, 1.0, 1.0, 1.0,
+                                  zp_y)
+        assert rc == 0
+        wt = ctx.prepare_weight(dev(w_kn), po.INT8, k, n, 0, scales=s_w, version=800 + m)
+        out = torch.empty((m, n), dtype=torch.int8, device="cuda")
+        ctx.i8_linear(po.I8_FC, dev(xq), 0.5, 0, m, wt, out, 1.0, zp_y)
+        got = out.cpu().numpy()
+        assert np.array_equal(got, ref), f"zp_y={zp_y} ({ctx.last_backend()}): {np.count_nonzero(got != ref)} mismatches"
+        wt.release()
