@@ -43,10 +43,13 @@ __device__ __forceinline__ int8_t requant_i8(double real, double s_out, double r
 
 // Requantization of an exact integer sum v (|v| < 2^24) with a per-column factor K = s_a * s_w / s_out held as
 // an unevaluated float pair kh + kl (K to ~2^-48): the code is clamp(round_half_away(v * K) + zp).  p = v * kh
-// and its exact rounding error e (one fma) give v * K = p + c, c = e + v * kl, to ~2^-45 |p|; with f = p - floor(p)
-// (exact for |p| < 2^23), d = (f - 0.5) + c has the sign of (v * K) - (floor(p) + 0.5) wherever |d| exceeds
-// 2^-36 (|p| + 1), and then the code is floor(p) + (d > 0) + zp, which is the reference's value (adding the
-// integer zp moves no x.5 point, and the reference's fp64 evaluation is within ~2^-50 of the exact value).
+// and its exact rounding error e (one fma) give v * K = p + c, c = e + v * kl, to ~2^-45 |p|.  With h =
+// floor(p) + 0.5 (exact), p - h lies in [-0.5, 0.5) and is exact wherever |p - h| <= 0.25 (Sterbenz: p and h
+// within a factor of two, or h = +-0.5 and p within 0.25 of it); elsewhere its rounding cannot change its
+// sign.  (p - floor(p) itself is not exact for p in (-1, 0): p + 1 needs more bits than p.)  So d = (p - h) + c
+// has the sign of v * K - h wherever |d| exceeds 2^-36 (|p| + 1), and then the code is floor(p) + (d > 0) + zp,
+// the reference's value (adding the integer zp moves no x.5 point, and the reference's fp64 evaluation is
+// within ~2^-50 of the exact value).
 // Otherwise (an x.5 point or closer than that, or |v| >= 2^24) `unsafe` is set and the caller decides with
 // the reference's arithmetic.  Magnitudes |p| >= 2^23 only ever clamp.
 __device__ __forceinline__ int8_t requant_i8_split(int32_t v, float kh, float kl, int32_t zp, bool& unsafe) {
@@ -56,7 +59,7 @@ __device__ __forceinline__ int8_t requant_i8_split(int32_t v, float kh, float kl
     const float e = __builtin_fmaf(vf, kh, -p);
     const float c = e + vf * kl;
     const float fl = floorf(p);
-    const float d = ((p - fl) - 0.5f) + c;
+    const float d = (p - (fl + 0.5f)) + c;
     unsafe = !(fabsf(d) > 0x1p-36f * (fabsf(p) + 1.0f)) || (uint32_t)(v + (1 << 24)) >= (2u << 24);
     const float r = fl + (d > 0.0f ? 1.0f : 0.0f) + (float)zp;
     const float hi = r < 127.0f ? r : 127.0f;

@@ -156,3 +156,26 @@ def test_i8_linear_near_ties(ctx, m):
         got = out.cpu().numpy()
         assert np.array_equal(got, ref), f"zp_y={zp_y} ({ctx.last_backend()}): {np.count_nonzero(got != ref)} mismatches"
         wt.release()
+
+
+@pytest.mark.parametrize("m", [100, 512])
+def test_i8_linear_value_just_above_minus_half(ctx, m):
+    """A sum whose v * K is -0.5 + 1.2e-8: fl32(v * kh) rounds to -0.49999997, where p - floor(p) = p + 1 is not
+    exact in fp32 (the float-pair form must use p - (floor(p) + 0.5)).  Reference code: round(17.500000012) = 18."""
+    k, n = 64, 128
+    xq = np.zeros((m, k), np.int8)
+    xq[:, 0], xq[:, 1] = -127, -1
+    w = np.zeros((n, k), np.int8)
+    w[:, 0], w[:, 1] = 27, 108  # dot = -3537 in every column
+    w[1::2, 1] = 107  # and -3429 - 107 = -3536 in odd columns
+    s_w = np.full(n, float.fromhex("0x1.fc2cp-8"), np.float32)
+    s_x, s_y = float.fromhex("0x1.2cdd28p-7"), float.fromhex("0x1.01dc72p-1")
+    w_kn = np.ascontiguousarray(w.T)
+    rc, ref, _ = po.i8_linear(po.I8_FC, xq, s_x, 0, w_kn, False, s_w, None, None, po.BIAS_NONE, 1.0, 1.0, s_y, 18)
+    assert rc == 0 and ref[0, 0] == 18
+    wt = ctx.prepare_weight(dev(w_kn), po.INT8, k, n, 0, scales=s_w, version=900 + m)
+    out = torch.empty((m, n), dtype=torch.int8, device="cuda")
+    ctx.i8_linear(po.I8_FC, dev(xq), s_x, 0, m, wt, out, s_y, 18)
+    got = out.cpu().numpy()
+    assert np.array_equal(got, ref), f"{ctx.last_backend()}: {np.count_nonzero(got != ref)} mismatches"
+    wt.release()

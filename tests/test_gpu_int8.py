@@ -423,3 +423,26 @@ def test_weight_zero_point_declines(ctx):
     y = torch.empty((1, 8, 9, 9), dtype=torch.int8, device="cuda")
     assert ctx.i8_conv2d(dev(x), 0, 0.5, 0, cw, y, 1.0, 0, pad=(1, 1), check=False) == -2
     cw.release()
+
+
+@pytest.mark.parametrize("kh", [1, 3])
+def test_i8_conv_value_just_above_minus_half(ctx, kh):
+    """Conv2D INT8 (64 input channels: the staged-window kernel) with every output's v * K = -0.5 + 1.2e-8,
+    where the float-pair requantization must not round p - floor(p); the reference's code is 18."""
+    c, oc, h, w_ = 64, 64, 8, 32
+    x = np.zeros((1, c, h, w_), np.int8)
+    x[0, 0], x[0, 1] = -127, -1
+    wt = np.zeros((oc, c, kh, kh), np.int8)
+    wt[:, 0, kh // 2, kh // 2], wt[:, 1, kh // 2, kh // 2] = 27, 108
+    s_w = np.full(oc, float.fromhex("0x1.fc2cp-8"), np.float32)
+    s_x, s_y = float.fromhex("0x1.2cdd28p-7"), float.fromhex("0x1.01dc72p-1")
+    pad = (kh // 2, kh // 2)
+    bias = np.zeros(oc, np.int32)
+    rc, ref = po.i8_conv2d(x, s_x, 0, wt, s_w, bias, (1, 1), pad, s_y, 18)
+    assert rc == 0 and ref[0, 0, h // 2, w_ // 2] == 18
+    wp = ctx.prepare_conv_weight(dev(wt), s_w, group=1, version=950 + kh)
+    out = torch.empty(ref.shape, dtype=torch.int8, device="cuda")
+    ctx.i8_conv2d(dev(x), 0, s_x, 0, wp, out, s_y, 18, stride=(1, 1), pad=pad, bias=dev(bias), bias_abs_max=0)
+    got = out.cpu().numpy()
+    assert np.array_equal(got, ref), f"{ctx.last_backend()}: {np.count_nonzero(got != ref)} mismatches"
+    wp.release()
