@@ -59,14 +59,22 @@ def fp8_spacing_table(dtype):
     return gaps
 
 
-def fp8_linear_check(dtype, got, ref, a_codes, sa, w_nk, sw, s_out, label=""):
+# Accumulation precision of the gfx950 FP8 MFMA (v_mfma_*_f8f6f4), measured: on sums near zero with heavy
+# cancellation its result differs from the exact sum by up to ~2^-14.6 * sum_k |a_k w_k| over a 64-deep block
+# (seeded comparison of 8,078 GEMMs, K = 16..4096, beyond the output code's own rounding), where fp32
+# summation in any order stays within 2 * (K-1) * 2^-24 of it.  MFMA backends get this term (with 2x room).
+FP8_MFMA_ACCUM_REL = 2.0 ** -13.6
+
+
+def fp8_linear_check(dtype, got, ref, a_codes, sa, w_nk, sw, s_out, label="", backend=""):
     """FP8-output tolerance of the linear path.
 
     An element passes when its code is within 1 FP8 code of the oracle's, or -- where cancellation
-    makes the fp32 accumulation-order error larger than an FP8 step (sums near zero) -- when the
-    decoded values differ by no more than the fp32 recursive-summation bound of both orders,
-    2 * (K-1) * 2^-24 * sum_k |a_k w_k|, plus one FP8 step.  A dropped, duplicated or
-    mis-indexed term moves an element by ~|a_k w_k| >> that bound and fails.
+    makes the accumulation error larger than an FP8 step (sums near zero) -- when the decoded values
+    differ by no more than the fp32 recursive-summation bound of both orders,
+    2 * (K-1) * 2^-24 * sum_k |a_k w_k|, plus one FP8 step, plus, for an MFMA backend (`backend` names
+    it), the MFMA's own accumulation error FP8_MFMA_ACCUM_REL * sum_k |a_k w_k|.  A dropped, duplicated
+    or mis-indexed term moves an element by ~|a_k w_k| (on average sum/K) and fails.
     Returns (exact-match rate, number of elements outside one code)."""
     d = fp8_code_distance(got, ref)
     far = np.nonzero(d > 1)
@@ -79,7 +87,8 @@ def fp8_linear_check(dtype, got, ref, a_codes, sa, w_nk, sw, s_out, label=""):
         g = got[far]
         r = ref[far]
         diff = np.abs(dec[g] - dec[r]) * s_out
-        bound = 2.0 * (k - 1) * 2.0 ** -24 * abs_sums[far] + np.maximum(gaps[g], gaps[r]) * s_out
+        rel = 2.0 * (k - 1) * 2.0 ** -24 + (FP8_MFMA_ACCUM_REL if "mfma" in backend else 0.0)
+        bound = rel * abs_sums[far] + np.maximum(gaps[g], gaps[r]) * s_out
         bad = diff > bound
         assert not np.any(bad), f"{label}: {int(bad.sum())} elements beyond the accumulation bound"
     exact = float(np.mean(d == 0))

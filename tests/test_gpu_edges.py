@@ -68,7 +68,7 @@ def test_fp8_linear_ragged_k(ctx, dtype, m):
     out = torch.empty((m, n), dtype=torch.uint8, device="cuda")
     ctx.fp8_linear(dev(xb.view(np.int16)), po.BF16, s_in, m, wt, sw, out, dtype, s_out)
     ref = po.fp8_gemm(dtype, a_codes, s_in, w_nk, sw, True, s_out)
-    fp8_linear_check(dtype, out.cpu().numpy(), ref, a_codes, s_in, w_nk, sw, s_out, f"ragged k m={m}")
+    fp8_linear_check(dtype, out.cpu().numpy(), ref, a_codes, s_in, w_nk, sw, s_out, f"ragged k m={m}", backend=ctx.last_backend())
     wt.release()
 
 
@@ -121,7 +121,7 @@ def test_fp8_gemm_activations_past_the_offset_limit(ctx):
                       r.choice(m, 16, replace=False))
     a_rows = a[torch.from_numpy(rows).cuda()].cpu().numpy()
     ref = po.fp8_gemm(dtype, a_rows, sa, w_nk, sw, True, s_out)
-    fp8_linear_check(dtype, out.cpu().numpy()[rows], ref, a_rows, sa, w_nk, sw, s_out, "gemm past 2^31")
+    fp8_linear_check(dtype, out.cpu().numpy()[rows], ref, a_rows, sa, w_nk, sw, s_out, "gemm past 2^31", backend=ctx.last_backend())
     del a, out
     torch.cuda.empty_cache()
     wt.release()

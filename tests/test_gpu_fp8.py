@@ -84,7 +84,7 @@ def test_fp8_gemv_matches_oracle(ctx, dtype, m, layout):
     ctx.fp8_linear(dev(a), dtype, sa, m, wt, sw, out, dtype, s_out)
     assert ctx.last_backend().startswith("fp8_gemv")
     ref = po.fp8_gemm(dtype, a, sa, w_nk, sw, True, s_out)
-    fp8_linear_check(dtype, host(out), ref, a, sa, w_nk, sw, s_out, f"gemv m={m}")
+    fp8_linear_check(dtype, host(out), ref, a, sa, w_nk, sw, s_out, f"gemv m={m}", backend=ctx.last_backend())
     wt.release()
 
 
@@ -101,7 +101,7 @@ def test_fp8_gemv_long_k_non_pow2_scale(ctx, dtype, m):
     ctx.fp8_linear(dev(a), dtype, sa, m, wt, sw, out, dtype, s_out)
     assert ctx.last_backend() == "fp8_gemv_mfma"
     ref = po.fp8_gemm(dtype, a, sa, w_nk, sw, True, s_out)
-    fp8_linear_check(dtype, host(out), ref, a, sa, w_nk, sw, s_out, f"gemv long k m={m}")
+    fp8_linear_check(dtype, host(out), ref, a, sa, w_nk, sw, s_out, f"gemv long k m={m}", backend=ctx.last_backend())
     wt.release()
 
 
@@ -128,7 +128,7 @@ def test_fp8_gemv_fused_bf16_io(ctx, dtype, m):
     got_codes = po.cast_to_fp8(po.BF16, got, dtype, s_out)  # bf16 of an fp8 value re-encodes exactly
     assert np.array_equal(po.cast_from_fp8(dtype, got_codes, s_out, po.BF16), got)
     fp8_linear_check(dtype, got_codes, ref_codes, a_codes, s_in, np.ascontiguousarray(w_codes.T), sw, s_out,
-                     "fused bf16")
+                     "fused bf16", backend=ctx.last_backend())
     assert np.mean(got == ref) > 0.97
     wt.release()
 
@@ -149,7 +149,7 @@ def test_fp8_mfma_gemm_matches_oracle(ctx, dtype, shape):
     ctx.fp8_linear(dev(a), dtype, sa, m, wt, sw, out, dtype, s_out)
     assert ctx.last_backend().startswith("fp8_mfma_gemm")
     ref = po.fp8_gemm(dtype, a[rows], sa, w_nk, sw, True, s_out)
-    fp8_linear_check(dtype, host(out)[rows], ref, a[rows], sa, w_nk, sw, s_out, f"gemm {shape}")
+    fp8_linear_check(dtype, host(out)[rows], ref, a[rows], sa, w_nk, sw, s_out, f"gemm {shape}", backend=ctx.last_backend())
     wt.release()
 
 
@@ -225,7 +225,7 @@ def test_fp8_gemm_decoded_outputs(ctx, dtype, out_dtype, shape):
     # sampled rows plus the last ones (m = 4000: a partial last row tile on the 256x224 path)
     rows = np.union1d(rng(9).choice(m, 64, replace=False), np.arange(m - 8, m))
     ref = po.fp8_gemm(dtype, a[rows], sa, w_nk, sw, True, s_out)
-    fp8_linear_check(dtype, codes[rows], ref, a[rows], sa, w_nk, sw, s_out, f"gemm out {out_dtype}")
+    fp8_linear_check(dtype, codes[rows], ref, a[rows], sa, w_nk, sw, s_out, f"gemm out {out_dtype}", backend=ctx.last_backend())
     wt.release()
 
 
@@ -291,7 +291,7 @@ def test_fp8_gemm_bias_alpha_beta_full_size(ctx):
                       alpha=0.5, beta=2.0)
     # the bias is added after the sum, in the reference's order, so only the sum's accumulation order differs;
     # alpha < 1 scales that error down, so the unscaled bound of fp8_linear_check holds
-    fp8_linear_check(dtype, host(out)[rows], ref, a[rows], sa, w_nk, sw, s_out, "gemm bias full size")
+    fp8_linear_check(dtype, host(out)[rows], ref, a[rows], sa, w_nk, sw, s_out, "gemm bias full size", backend=ctx.last_backend())
     wt.release()
 
 
@@ -362,7 +362,7 @@ def test_fp8_gemm_special_values_and_saturation(ctx, dtype, shape, mode):
     ordinary = np.setdiff1d(np.arange(rows.size), [int(np.nonzero(rows == r)[0][0]) for r in special_rows])
     fp8_linear_check(dtype, np.where(keep, got, 0)[ordinary].astype(np.uint8),
                      np.where(keep, ref, 0)[ordinary].astype(np.uint8), a[rows][ordinary], sa, w_nk, sw, s_out,
-                     f"special {shape} {mode}")
+                     f"special {shape} {mode}", backend=ctx.last_backend())
     wt.release()
 
 
@@ -386,7 +386,7 @@ def test_fp8_gemv_fp32_input_ragged_k(ctx, dtype, m, k):
     ctx.fp8_linear(dev(x), po.FP32, s_in, m, wt, sw, out, dtype, s_out)
     assert ctx.last_backend() == "fp8_gemv_mfma"
     ref = po.fp8_gemm(dtype, a_codes, s_in, w_codes, sw, True, s_out)
-    fp8_linear_check(dtype, host(out), ref, a_codes, s_in, w_codes, sw, s_out, f"gemv fp32 m={m} k={k}")
+    fp8_linear_check(dtype, host(out), ref, a_codes, s_in, w_codes, sw, s_out, f"gemv fp32 m={m} k={k}", backend=ctx.last_backend())
     wt.release()
 
 
@@ -412,5 +412,5 @@ def test_fp8_gemv_m1_k_tails(ctx, dtype, src, k):
     ctx.fp8_linear(dev(xin), src, s_in, 1, wt, sw, out, dtype, s_out)
     assert ctx.last_backend() == "fp8_gemv_m1"
     ref = po.fp8_gemm(dtype, a_codes, s_in, w_codes, sw, True, s_out)
-    fp8_linear_check(dtype, host(out), ref, a_codes, s_in, w_codes, sw, s_out, f"gemv m1 k={k}")
+    fp8_linear_check(dtype, host(out), ref, a_codes, s_in, w_codes, sw, s_out, f"gemv m1 k={k}", backend=ctx.last_backend())
     wt.release()

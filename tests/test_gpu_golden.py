@@ -97,13 +97,13 @@ def test_fp8_linear_matches_golden(ctx, name, dtype):
     wt = ctx.prepare_weight(dev(w_nk), dtype, k, n, 1, version=30)
     out = torch.empty((m, n), dtype=torch.uint8, device="cuda")
     ctx.fp8_linear(dev(a), dtype, sa, m, wt, sw, out, dtype, s_out)
-    fp8_linear_check(dtype, out.cpu().numpy(), g[f"{name}_direct_t1"], a, sa, w_nk, sw, s_out, "HIP vs reference")
+    fp8_linear_check(dtype, out.cpu().numpy(), g[f"{name}_direct_t1"], a, sa, w_nk, sw, s_out, "HIP vs reference", backend=ctx.last_backend())
     rows = []
     for i in range(m):  # the decode path, one row per call, against the reference's prepared M = 1 kernel
         o1 = torch.empty((1, n), dtype=torch.uint8, device="cuda")
         ctx.fp8_linear(dev(a[i:i + 1]), dtype, sa, 1, wt, sw, o1, dtype, s_out)
         rows.append(o1.cpu().numpy()[0])
-    fp8_linear_check(dtype, np.stack(rows), g[f"{name}_packed"], a, sa, w_nk, sw, s_out, "HIP m=1 vs reference")
+    fp8_linear_check(dtype, np.stack(rows), g[f"{name}_packed"], a, sa, w_nk, sw, s_out, "HIP m=1 vs reference", backend=ctx.last_backend())
     wt.release()
 
 

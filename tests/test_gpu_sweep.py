@@ -132,7 +132,7 @@ def test_sweep_fp8_linear(ctx, seed):
     ctx.fp8_linear(dev(a), dtype, sa, m, wt, sw, out, dtype, s_out)
     ref = po.fp8_gemm(dtype, a, sa, w_nk, sw, True, s_out)
     fp8_linear_check(dtype, out.cpu().numpy(), ref, a, sa, w_nk, sw, s_out,
-                     f"sweep m={m} k={k} n={n} layout={layout} ({ctx.last_backend()})")
+                     f"sweep m={m} k={k} n={n} layout={layout} ({ctx.last_backend()})", backend=ctx.last_backend())
     wt.release()
 
 
