@@ -144,7 +144,10 @@ __device__ __forceinline__ float scaled(const Fp8Epilogue& ep, float mul, float 
         return (acc * ep.ab_scale * ep.alpha) / ep.out_scale;
     } else {
         float y = acc * ep.ab_scale * ep.alpha;
-        const uint8_t bc = ep.bias[ep.bias_kind == FHIP_BIAS_VECTOR ? col : row * ep.n + col];
+        // the tile epilogue evaluates positions past n (and past m: the caller clamps the row) that are never
+        // stored; their bias index is clamped into the bias, which holds exactly n (vector) or m * n values
+        const int64_t bcol = col < ep.n ? col : ep.n - 1;
+        const uint8_t bc = ep.bias[ep.bias_kind == FHIP_BIAS_VECTOR ? bcol : row * ep.n + bcol];
         y += ep.beta * (fhip::fp8_decode(bc, E5) * ep.bias_scale);
         return SM == kScalePow2 ? y * ep.out_inv : y / ep.out_scale;
     }
@@ -488,7 +491,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
                 const int c = wcol + j * 32 + g * 8 + col_q;
                 const float v4[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
                 uint32_t packed[OUT_BYTES];
-                fast_value4<E5, SM, BIAS, OUT_BYTES, FIX>(ep, mul, v4, m0 + r, n0 + c, packed, flag);
+                // rows past m are computed, never stored: their bias row is clamped to the last one
+                const int64_t brow = m0 + r < m ? m0 + r : m - 1;
+                fast_value4<E5, SM, BIAS, OUT_BYTES, FIX>(ep, mul, v4, brow, n0 + c, packed, flag);
                 uint8_t* dst = so + r * kOutPitch + c * OUT_BYTES;
                 if constexpr (OUT_BYTES == 1) *reinterpret_cast<uint32_t*>(dst) = packed[0];
                 else if constexpr (OUT_BYTES == 2) *reinterpret_cast<uint2*>(dst) = make_uint2(packed[0], packed[1]);

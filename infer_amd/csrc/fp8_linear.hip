@@ -104,6 +104,8 @@ __device__ __forceinline__ void stage_activations(const void* __restrict__ a, in
                 *reinterpret_cast<uint32_t*>(xs + g * 4) = c;
             }
         }
+        // a thread with no activation group (mt * kp / 4 < threads) still issues its first weight batch
+        if (first) after_first_loads();
     } else {
         after_first_loads();
         for (int64_t idx = tid; idx < (int64_t)mt * kp; idx += kGemvThreads) {

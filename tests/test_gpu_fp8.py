@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from oracle import pyoracle as po
-from tests.common import SEEDS, fp8_code_distance, fp8_linear_check, fp8_tensor, rng, same_float_bits
+from tests.common import SEEDS, fp8_code_distance, fp8_linear_check, fp8_pow2_scale, fp8_tensor, rng, same_float_bits
 
 pytestmark = pytest.mark.gpu
 
@@ -413,4 +413,49 @@ def test_fp8_gemv_m1_k_tails(ctx, dtype, src, k):
     assert ctx.last_backend() == "fp8_gemv_m1"
     ref = po.fp8_gemm(dtype, a_codes, s_in, w_codes, sw, True, s_out)
     fp8_linear_check(dtype, host(out), ref, a_codes, s_in, w_codes, sw, s_out, f"gemv m1 k={k}", backend=ctx.last_backend())
+    wt.release()
+
+
+@pytest.mark.parametrize("bias_kind", [po.BIAS_VECTOR, po.BIAS_MATRIX])
+@pytest.mark.parametrize("m,k,n", [(40, 912, 578), (300, 176, 174)])
+def test_fp8_gemm_bias_partial_tiles(ctx, bias_kind, m, k, n):
+    """Bias on the tile GEMM with partial tiles in M and N: the epilogue evaluates positions past m and n
+    (never stored) and must read the bias only inside its m x n (or n) values; general output scale."""
+    dtype = po.FP8E4M3
+    a, sa, w_nk, w_src, sw, s_out = _linear_case(31, dtype, m, k, n, 1)
+    s_out = float(np.float32(s_out * 0.7))  # not a power of two: the general scale mode
+    shape = (n,) if bias_kind == po.BIAS_VECTOR else (m, n)
+    bias, sb = fp8_tensor(rng(32).standard_normal(shape).astype(np.float32) * 0.05, dtype)
+    wt = ctx.prepare_weight(dev(w_src), dtype, k, n, 1, version=11)
+    out = torch.empty((m, n), dtype=torch.uint8, device="cuda")
+    ctx.fp8_linear(dev(a), dtype, sa, m, wt, sw, out, dtype, s_out, bias=dev(bias), bias_scale=sb,
+                   bias_kind=bias_kind, alpha=0.5, beta=2.0)
+    assert ctx.last_backend().startswith("fp8_mfma_gemm_")
+    ref = po.fp8_gemm(dtype, a, sa, w_nk, sw, True, s_out, bias=bias, s_bias=sb, bias_kind=bias_kind, alpha=0.5,
+                      beta=2.0)
+    fp8_linear_check(dtype, host(out), ref, a, sa, w_nk, sw, s_out, f"gemm bias {bias_kind} {m}x{k}x{n}",
+                     backend=ctx.last_backend())
+    wt.release()
+
+
+@pytest.mark.parametrize("k", [128, 368, 800])
+def test_fp8_gemv_m1_general_output_scale_short_k(ctx, k):
+    """m = 1 with a non power-of-two output scale runs the LDS-staged MFMA GEMV; with m * kp / 4 below the
+    block's 256 threads some threads stage no activations and must still issue their first weight batch."""
+    dtype = po.FP8E4M3
+    n = 272
+    r = rng(33 + k)
+    x = r.standard_normal((1, k)).astype(np.float32)
+    w_nk, sw = fp8_tensor((r.standard_normal((n, k)) * 0.02).astype(np.float32), dtype)
+    s_in = fp8_pow2_scale(float(np.max(np.abs(x))), dtype)
+    a_codes = po.cast_to_fp8(po.FP32, x, dtype, s_in)
+    s_out = float(np.float32(fp8_pow2_scale(float(np.max(np.abs(po.fp8_sums(dtype, a_codes, s_in, w_nk, sw, True)))),
+                                            dtype) * 0.8))
+    wt = ctx.prepare_weight(dev(w_nk), dtype, k, n, 1, version=12)
+    out = torch.empty((1, n), dtype=torch.uint8, device="cuda")
+    ctx.fp8_linear(dev(x), po.FP32, s_in, 1, wt, sw, out, dtype, s_out)
+    assert ctx.last_backend() == "fp8_gemv_mfma"
+    ref = po.fp8_gemm(dtype, a_codes, s_in, w_nk, sw, True, s_out)
+    fp8_linear_check(dtype, host(out), ref, a_codes, s_in, w_nk, sw, s_out, f"gemv m1 general k={k}",
+                     backend=ctx.last_backend())
     wt.release()
