@@ -64,7 +64,7 @@ def test_i8_tile_gemm_bitexact(ctx, case):
 
 
 @pytest.mark.parametrize("out_dtype", [po.FP32, po.FP16, po.BF16])
-@pytest.mark.parametrize("m,k,n", [(600, 512, 1000), (2048, 256, 3000)])
+@pytest.mark.parametrize("m,k,n", [(600, 512, 1000), (2048, 256, 3000), (4000, 128, 3500)])
 def test_i8_tile_gemm_fused_dequantize(ctx, out_dtype, m, k, n):
     r = rng(m + n + out_dtype)
     xq = r.integers(-128, 128, (m, k)).astype(np.int8)
