@@ -811,8 +811,10 @@ int fhip_i8_linear_ex(fhip_context ctx, int kind, const int8_t* a, float s_a, in
     // Large M: the LDS-staged MFMA tile GEMM (operand reuse across a 128x128 or 256x256 tile).
     const bool tile_rows =
         m >= kI8TileMinRows || (m >= kI8TileMinRowsLarge && (double)m * (double)w->n * (double)w->k >= kI8TileMinMacs);
+    // (its buffer resources address the activations and the prepared weight with 32-bit offsets)
+    const int64_t tile_wbytes = ((w->n + 255) / 256 * 256) * ((w->k + 127) / 128 * 128);
     if (tile_rows && w->k % 64 == 0 && (reinterpret_cast<uintptr_t>(a) & 15) == 0 &&
-        m * w->k < (int64_t(1) << 31))
+        m * w->k < (int64_t(1) << 31) && tile_wbytes < (int64_t(1) << 31))
         return fhip::launch_i8_gemm_tile(ctx, a, m, w, ep);
     const int64_t kp = ((w->k + 127) / 128) * 128;
     // largest tile that still puts about two blocks on every CU
