@@ -536,6 +536,17 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
         const int32_t zp_out_i = (int32_t)iep.zp_out;
         const float zp_half = (float)zp_out_i + 0.5f;
         const int32_t* colp = reinterpret_cast<const int32_t*>(smem + kColOff);
+        // NT is a multiple of the chunks per row, so a thread's chunk (its four columns) is the same in every
+        // pass and slab: their parameters are read once
+        static_assert(NT % kChunksRow == 0, "one chunk per thread");
+        const int chunk = tid % kChunksRow, c = chunk * 4;
+        const int64_t col = n0 + c;
+        const int nv = cols_in - c < 4 ? cols_in - c : 4;
+        const int4 p0 = *reinterpret_cast<const int4*>(colp + c);
+        const int4 p1 = *reinterpret_cast<const int4*>(colp + BN + c);
+        const int4 p2 = *reinterpret_cast<const int4*>(colp + 2 * BN + c);
+        const int a0[4] = {p0.x, p0.y, p0.z, p0.w}, a1[4] = {p1.x, p1.y, p1.z, p1.w};
+        const int a2[4] = {p2.x, p2.y, p2.z, p2.w};
         static_for<FM>([&](auto ii) {
             constexpr int i = decltype(ii)::value;
             if (i > 0) __syncthreads();  // the previous slab has been read
@@ -549,20 +560,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
                 });
             });
             __syncthreads();
-            for (int q = tid; q < kSlabRows * kChunksRow; q += NT) {
-                const int srow = q / kChunksRow, chunk = q % kChunksRow;
+            for (int srow = tid / kChunksRow; srow < kSlabRows && c < cols_in; srow += NT / kChunksRow) {
                 const int r = (srow >> 5) * WTM + i * 32 + (srow & 31);
-                const int c = chunk * 4;
-                if (r >= rows_in || c >= cols_in) continue;
+                if (r >= rows_in) continue;
                 const int4 raw4 = *reinterpret_cast<const int4*>(slab_at(srow, chunk));
                 const int raw[4] = {raw4.x, raw4.y, raw4.z, raw4.w};
-                const int4 p0 = *reinterpret_cast<const int4*>(colp + c);
-                const int4 p1 = *reinterpret_cast<const int4*>(colp + BN + c);
-                const int4 p2 = *reinterpret_cast<const int4*>(colp + 2 * BN + c);
-                const int a0[4] = {p0.x, p0.y, p0.z, p0.w}, a1[4] = {p1.x, p1.y, p1.z, p1.w};
-                const int a2[4] = {p2.x, p2.y, p2.z, p2.w};
-                const int64_t row = m0 + r, col = n0 + c;
-                const int nv = cols_in - c < 4 ? cols_in - c : 4;
+                const int64_t row = m0 + r;
                 int8_t qv[4];
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
