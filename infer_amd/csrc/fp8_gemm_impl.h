@@ -81,7 +81,7 @@ template <int BM, int BN, int NT, int OUT_BYTES, int BK, int STAGES, bool I8 = f
 constexpr size_t lds_bytes() {
     constexpr size_t ops = (size_t)STAGES * Stage<BM, BN, NT, BK>::kBytes;
     constexpr size_t epi = (size_t)BM * (BN * OUT_BYTES + 16);
-    return (ops > epi ? ops : epi) + (I8 ? (size_t)BN * 12 : 0);
+    return (ops > epi ? ops : epi) + (I8 ? (size_t)((BN + 63) / 64 * 64) * 12 : 0);
 }
 
 template <int BK>
@@ -298,9 +298,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
     // with 4-byte buffer_load ... lds, issued before any stage load: every later vmcnt wait of the main
     // loop covers them.  Columns past n read as zero and are never stored.
     constexpr size_t kColOff = lds_bytes<BM, BN, NT, OUT_BYTES, BK, STAGES, false>();
+    // column arrays of the INT8 mode: BN rounded up to 64 entries (whole 64-lane DMA loads; BN = 224 tiles)
+    constexpr int BNR = (BN + 63) / 64 * 64;
     if constexpr (I8) {
-        static_assert(BN % 64 == 0, "INT8 mode: BN a multiple of 64");
-        constexpr int kParts = BN / 64;
+        constexpr int kParts = BNR / 64;
         const int cols = (int)(iep.ldo - n0 < BN ? iep.ldo - n0 : BN);
         for (int q = wave; q < 3 * kParts; q += NT / 64) {
             const int arr = q / kParts, part = q % kParts;
@@ -309,7 +310,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
             const int bytes = arr == 1 && iep.bias_kind != FHIP_BIAS_VECTOR ? 0 : cols * 4;
             const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
                 (void*)(static_cast<const uint8_t*>(src) + (bytes ? n0 * 4 : 0)), 0, bytes, kBufferRsrcWord3);
-            uint8_t* dst = smem + kColOff + (size_t)arr * BN * 4 + part * 256;
+            uint8_t* dst = smem + kColOff + (size_t)arr * BNR * 4 + part * 256;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 4, (uint32_t)(part * 256 + lane * 4), 0, 0, 0);
         }
     }
@@ -464,10 +465,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
             int32_t* cw = reinterpret_cast<int32_t*>(smem + kColOff);
             for (int c = tid; c < BN; c += NT) {
                 float kh, kl;
-                iep.split_scale(reinterpret_cast<const float*>(cw + 2 * BN)[c], kh, kl);
-                cw[c] = (iep.bias_kind == FHIP_BIAS_VECTOR ? cw[BN + c] : 0) - iep.zp_a * cw[c];
-                reinterpret_cast<float*>(cw + BN)[c] = kl;
-                reinterpret_cast<float*>(cw + 2 * BN)[c] = kh;
+                iep.split_scale(reinterpret_cast<const float*>(cw + 2 * BNR)[c], kh, kl);
+                cw[c] = (iep.bias_kind == FHIP_BIAS_VECTOR ? cw[BNR + c] : 0) - iep.zp_a * cw[c];
+                reinterpret_cast<float*>(cw + BNR)[c] = kl;
+                reinterpret_cast<float*>(cw + 2 * BNR)[c] = kh;
             }
         }
     }
@@ -522,14 +523,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
         // 128 accumulators of a lane, the same work held the whole accumulator set live through a long
         // branchy tail and spilled.  The integer path decides each code with requant_i8_split; values it
         // cannot decide (x.5 points) take the reference's fp64 arithmetic in place.
-        static_assert(WTN1 == 0, "INT8 mode: equal wave columns");
         constexpr int kSlabRows = WAVES_M * 32;
-        constexpr int kChunksRow = BN / 4;  // 16-byte chunks of int32 per staged row
-        static_assert((size_t)kSlabRows * BN * 4 <= kColOff, "INT8 slab must not reach the column parameters");
+        constexpr int kChunksRow = BNR / 4;  // 16-byte chunks of int32 per staged row (past BN: never read)
+        static_assert((size_t)kSlabRows * BNR * 4 <= kColOff, "INT8 slab must not reach the column parameters");
         int32_t* const slab = reinterpret_cast<int32_t*>(smem);
         // chunk swizzle: the 32 rows of one ds_write_b128 group land on distinct 16-byte bank groups
         auto slab_at = [&](int srow, int chunk) __attribute__((always_inline)) {
-            return slab + srow * BN + ((chunk ^ ((srow & (kChunksRow / 2 - 1)) << 1)) << 2);
+            return slab + srow * BNR + ((chunk ^ ((srow & (kChunksRow / 2 - 1)) << 1)) << 2);
         };
         const int rows_in = (int)(m - m0 < BM ? m - m0 : BM);
         const int cols_in = (int)(iep.ldo - n0 < BN ? iep.ldo - n0 : BN);
@@ -543,8 +543,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(const 
         const int64_t col = n0 + c;
         const int nv = cols_in - c < 4 ? cols_in - c : 4;
         const int4 p0 = *reinterpret_cast<const int4*>(colp + c);
-        const int4 p1 = *reinterpret_cast<const int4*>(colp + BN + c);
-        const int4 p2 = *reinterpret_cast<const int4*>(colp + 2 * BN + c);
+        const int4 p1 = *reinterpret_cast<const int4*>(colp + BNR + c);
+        const int4 p2 = *reinterpret_cast<const int4*>(colp + 2 * BNR + c);
         const int a0[4] = {p0.x, p0.y, p0.z, p0.w}, a1[4] = {p1.x, p1.y, p1.z, p1.w};
         const int a2[4] = {p2.x, p2.y, p2.z, p2.w};
         static_for<FM>([&](auto ii) {

@@ -13,6 +13,11 @@ int launch_i8(fhip_context ctx, const uint8_t* a, int64_t m, const fhip_weight_s
     const int64_t n = w->n, k = w->k;
     const bool big = ((m + 255) / 256) * ((n + 255) / 256) >= 192 && OB != 4;
     if (k % 128 == 0) {
+        // N a multiple of 224 (Qwen's 3584 = 16 x 224): 256x224 tiles (two wave columns of 128 and 96), so the
+        // tile count is a multiple of 16 rather than 14
+        if (big && n % 224 == 0)
+            return launch_tile<false, OB, 256, 224, 4, 2, 128, 2, 96, true>(ctx, a, m, k, w, ep,
+                                                                           "i8_mfma_gemm_256x224_bk128_w8", &iep);
         if (big)
             return launch_tile<false, OB, 256, 256, 4, 2, 128, 2, 0, true>(ctx, a, m, k, w, ep,
                                                                           "i8_mfma_gemm_256x256_bk128_w8", &iep);

@@ -27,6 +27,8 @@ CASES = [
     (3100, 320, 3900, po.I8_FC, po.BIAS_VECTOR, -3, 2, 1.0, 1.0, True, "i8_mfma_gemm_256x256_w8"),
     (385, 128, 33, po.I8_MATMUL, po.BIAS_NONE, 12, 0, 1.0, 1.0, False, "i8_mfma_gemm_128x128_bk128_w8"),
     (777, 64, 515, po.I8_GEMM, po.BIAS_NONE, 0, -1, 2.0, 0.0, True, "i8_mfma_gemm_128x128_w8"),
+    (4000, 128, 3584, po.I8_FC, po.BIAS_VECTOR, 9, -6, 1.0, 1.0, False, "i8_mfma_gemm_256x224_bk128_w8"),
+    (4000, 256, 3584, po.I8_GEMM, po.BIAS_MATRIX, -4, 3, 1.0, 1.0, True, "i8_mfma_gemm_256x224_bk128_w8"),
 ]
 
 
@@ -64,7 +66,7 @@ def test_i8_tile_gemm_bitexact(ctx, case):
 
 
 @pytest.mark.parametrize("out_dtype", [po.FP32, po.FP16, po.BF16])
-@pytest.mark.parametrize("m,k,n", [(600, 512, 1000), (2048, 256, 3000), (4000, 128, 3500)])
+@pytest.mark.parametrize("m,k,n", [(600, 512, 1000), (2048, 256, 3000), (4000, 128, 3500), (4000, 128, 3584)])
 def test_i8_tile_gemm_fused_dequantize(ctx, out_dtype, m, k, n):
     r = rng(m + n + out_dtype)
     xq = r.integers(-128, 128, (m, k)).astype(np.int8)
